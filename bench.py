@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+Default workload (decode_256): one layer of a ragged decode step of Llama-3.1-8B's attention shape
+(32 query / 8 KV heads, head_dim 128, 16-token blocks, bf16) over 256 rows whose cached contexts are
+uniform in [128, 4096], one new token each, pool = 2x the pages with a shuffled assignment.  A step
+is KV append + split-KV paged decode + split merge, with the step's metadata and work plan built
+beforehand (they are built once per engine step and shared by all 32 layers; their cost is reported
+separately).  `value` is decode tokens/s of the 32-layer model: 256 / (32 x layer time).
+
+Prints one JSON line with the roofline of the dominant kernel (the decode kernel: algorithmic bytes
+per launch / its mean duration from HIP events around each launch in the timed region) and a CPU
+baseline: the oracle's restatement of the reference torch backend (gather + SDPA, bf16) timed on this
+host's cores on a bounded sample of the same rows.
+
+    python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "mini-llm-inference-server_amd"), str(ROOT / "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "ragged paged-attn decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 256 seqs"
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+LAYERS = 32
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="decode_256")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-rows", type=int, default=16)
+    return ap.parse_args()
+
+
+def cpu_baseline(wl, rows: int):
+    """The oracle (reference torch backend restated: write_kv, gather, SDPA; bf16) on this host's cores
+    over the first `rows` rows of the workload, same pool and tensors."""
+    import torch
+
+    from harness import oracle_step
+    from minillm.workloads import Workload
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    sel = list(range(min(rows, len(wl.seqs))))
+    starts = [0]
+    for c, n, _ in wl.seqs:
+        starts.append(starts[-1] + n)
+    tok = [t for i in sel for t in range(starts[i], starts[i + 1])]
+    sub = Workload(wl.name + "_sample", [wl.seqs[i] for i in sel], wl.num_blocks, wl.q[tok], wl.k[tok], wl.v[tok],
+                   wl.pool_k, wl.pool_v)
+    oracle_step(sub, "cpu", dtype=torch.bfloat16)  # warm-up
+    times, t_end = [], time.perf_counter() + 20.0
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        oracle_step(sub, "cpu", dtype=torch.bfloat16)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    n_tok = len(tok)
+    return {"value": n_tok / (LAYERS * t), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {len(sel)} of {len(wl.seqs)} rows, one layer x {len(times)} reps (median "
+                      f"{t * 1e3:.1f} ms), scaled to {LAYERS} layers; effective "
+                      f"{sub.algorithmic_bytes() / t / 1e9:.2f} GB/s on the same algorithmic bytes"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build runs the paged hot path on a single MI355X "
+              "(sharding is described, not built); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from minillm import workloads
+    from minillm.attention.hip_backend import HipBackend
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    dev = torch.device("cuda:0")
+    wl = workloads.WORKLOADS[args.workload]()
+    q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
+    pool_k, pool_v = wl.pool_k.to(dev), wl.pool_v.to(dev)
+    seqs = [SeqStep(c, n, b) for c, n, b in wl.seqs]
+    backend = HipBackend()
+
+    # per-step costs shared by the 32 layers: metadata build (host + GPU) and the GPU work plan
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        meta = AttentionMetadata.build(seqs, wl.block_size, dev)
+        backend._planned = None
+        backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+    torch.cuda.synchronize()
+    meta_plan_ms = (time.perf_counter() - t0) / 5 * 1e3
+
+    out = torch.empty_like(q)
+    plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+
+    def step(ev=None):
+        backend.append(k, v, pool_k, pool_v, meta)
+        if plan.num_decode:
+            if ev is not None:
+                ev[0].record()
+            backend.run_decode(q, pool_k, pool_v, meta, out)
+            if ev is not None:
+                ev[1].record()
+            backend.run_merge(q, meta, out)
+        if plan.num_prefill:
+            if ev is not None:
+                ev[2].record()
+            backend.run_prefill(q, pool_k, pool_v, meta, out)
+            if ev is not None:
+                ev[3].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps between two synchronisations; per-launch events around the dominant kernels
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        step(evs[i])
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1e3
+    step_ms = start.elapsed_time(stop) / args.steps
+    dec_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0
+    pf_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0
+
+    n_rows = len(wl.seqs)
+    step_bytes = wl.algorithmic_bytes()
+    per_layer_tok_s = wl.num_tokens / (step_ms * 1e-3)
+    value = wl.num_tokens / (LAYERS * step_ms * 1e-3)
+    if plan.num_decode:
+        dec_bytes = wl.decode_kernel_bytes()
+        achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
+        traffic = None
+        tfile = ROOT / "profiles" / f"decode_kernel_{wl.name}_traffic.json"
+        if tfile.exists():
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                    "kernel": "decode_kernel", "algorithmic_bytes": dec_bytes, "mean_us": round(dec_ms * 1e3, 2)}
+    else:
+        flops = wl.prefill_flops()
+        achieved = flops / (pf_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "prefill_kernel",
+                    "algorithmic_flops": flops, "mean_us": round(pf_ms * 1e3, 2)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{wl.name}: one attention layer of Llama-3.1-8B shape (32/8 heads, d=128, block 16,"
+                               f" bf16), {n_rows} rows, {wl.num_tokens} new tokens; step = KV append + paged "
+                               f"attention (+ split merge); value = tokens/s scaled to {LAYERS} layers",
+                   "rows": n_rows, "new_tokens": wl.num_tokens, "context_tokens": sum(wl.lens),
+                   "pages_per_split": plan.pages_per_split, "decode_items": plan.num_decode,
+                   "prefill_items": plan.num_prefill},
+        "roofline": roofline,
+        "per_layer": {"tokens_per_s": round(per_layer_tok_s, 1), "algorithmic_bytes": step_bytes,
+                      "hbm_gbps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+                      "hbm_frac": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                      "decode_us": round(dec_ms * 1e3, 2), "prefill_us": round(pf_ms * 1e3, 2),
+                      "prefill_tflops": round(wl.prefill_flops() / (pf_ms * 1e-3) / 1e12, 1) if pf_ms else None},
+        "per_step_shared_ms": {"metadata_build_and_plan": round(meta_plan_ms, 3)},
+        "wall_ms_timed_region": round(wall_ms, 2),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_rows)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

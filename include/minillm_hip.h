@@ -1,0 +1,163 @@
+/*
+ * minillm_hip.h — C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * Every entry point takes raw device pointers, explicit sizes and element strides, and a HIP stream
+ * (passed as void*), launches asynchronously on that stream and never synchronises the host.  The
+ * library never allocates device memory: the caller (PyTorch, in the host package) owns every buffer,
+ * including the decode workspace whose size mllm_decode_workspace_bytes() reports.
+ *
+ * Status: 0 on success, negative on failure; mllm_last_error() then returns a per-thread message.
+ *   MLLM_ERR_INVALID     malformed arguments            (the Python wrapper raises ValueError)
+ *   MLLM_ERR_UNSUPPORTED shape or dtype not supported   (ValueError)
+ *   MLLM_ERR_HIP         a HIP launch or runtime error  (RuntimeError)
+ *
+ * The pool layout is the reference's (cache/paged.py:24-31): per layer, separate K and V tensors
+ * [num_blocks, block_size, Hkv, Dh], contiguous (NHD: token-major inside a block); the flat slot of
+ * token p of a sequence is block_ids[p / block_size] * block_size + p % block_size.
+ */
+#ifndef MINILLM_HIP_H
+#define MINILLM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLLM_ABI_VERSION 1
+
+#define MLLM_OK 0
+#define MLLM_ERR_INVALID (-1)
+#define MLLM_ERR_UNSUPPORTED (-2)
+#define MLLM_ERR_HIP (-3)
+
+/* element types (torch.float32, torch.float16, torch.bfloat16) */
+#define MLLM_DTYPE_F32 0
+#define MLLM_DTYPE_F16 1
+#define MLLM_DTYPE_BF16 2
+
+/* ABI version of the loaded library (MLLM_ABI_VERSION at build time). */
+int mllm_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mllm_last_error(void);
+
+/*
+ * Ragged metadata build, on the GPU.
+ * Replaces the host loops and eleven host->device copies of AttentionMetadata.build
+ * (reference src/minillm/attention/metadata.py:70-103) with one upload of the block manager's tables
+ * and two launches.
+ *
+ * Inputs (device, int32): num_cached[S], num_new[S] (reference SeqStep, metadata.py:27-33), and each
+ * sequence's block table in CSR form: table_indptr[S+1] into table_ids[].  The caller has checked that
+ * every table holds its sequence (metadata.py:75-76 raises ValueError otherwise) and passes
+ * table_width = max table length.
+ * Outputs (device), bit-identical in dtype and value to the reference fields (metadata.py:93-102):
+ *   int64 positions[N], slot_mapping[N], block_tables[S * table_width] (row-major, padded with 0),
+ *         logits_index[S]
+ *   int32 qo_indptr[S+1], seq_lens[S], block_tables_i32[S * table_width], kv_indptr[S+1],
+ *         kv_indices[sum ceil(len/bs)], kv_last_page_len[S]
+ * N = sum num_new.  Any output pointer may be NULL to skip that field, except qo_indptr and kv_indptr.
+ */
+int mllm_build_metadata(const int32_t* num_cached, const int32_t* num_new, const int32_t* table_indptr,
+                        const int32_t* table_ids, int32_t num_seqs, int32_t block_size, int32_t table_width,
+                        int64_t* positions, int64_t* slot_mapping, int64_t* block_tables, int64_t* logits_index,
+                        int32_t* qo_indptr, int32_t* seq_lens, int32_t* block_tables_i32, int32_t* kv_indptr,
+                        int32_t* kv_indices, int32_t* kv_last_page_len, void* stream);
+
+/*
+ * KV append: scatter N new K and V rows into the pool at slot_mapping.
+ * Replaces write_kv (reference src/minillm/attention/paged_torch_ref.py:23-28), i.e.
+ *   k_cache.view(-1, Hkv, Dh).index_copy_(0, slot_mapping, k.to(k_cache.dtype)), same for v.
+ * k, v: [N, Hkv, Dh] with element strides (stride_tok, stride_head) and unit stride on Dh.
+ * The value conversion when src_dtype != cache_dtype rounds to nearest even, as torch's .to() does.
+ * Bit-exact.  Slots outside [0, num_slots) are not written.
+ */
+int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
+                   int64_t v_stride_head, int32_t src_dtype, void* k_cache, void* v_cache, int32_t cache_dtype,
+                   int64_t num_slots, int32_t num_kv_heads, int32_t head_dim, const int64_t* slot_mapping,
+                   int64_t num_tokens, void* stream);
+
+/*
+ * Per-step work plan (the analogue of FlashInfer's plan(), which the reference runs once per step:
+ * src/minillm/attention/flashinfer_backend.py:44-64).  Built on the GPU from qo_indptr / kv_indptr.
+ *   decode rows (num_new == 1): split into chunks of pages_per_split pages; one int4 work item
+ *     {seq, split, num_splits, first_item} each, in sequence order -> decode_work[num_decode_work];
+ *     sequences with more than one split also get an int4 {seq, first_item, num_splits, 0}
+ *     -> merge_work[num_merge_work].
+ *   multi-token rows: one int2 item {seq, first_new_token} per tile of q_tile_tokens new tokens,
+ *     last tile of each row first -> prefill_work[num_prefill_work].
+ * The caller computes the three counts from the same host facts (sequence lengths and new-token
+ * counts); the kernel writes at most that many items.  pages_per_split <= 64.
+ */
+int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, int32_t pages_per_split,
+              int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work,
+              int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work, void* stream);
+
+/* Bytes of fp32 split-KV partials the decode needs for num_decode_work items (0 if none split). */
+int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim);
+
+/*
+ * Paged decode attention: one new token per row, over its whole context in the pool
+ * (reference src/minillm/attention/paged_torch_ref.py:47-59, decode branch; FlashInfer
+ * BatchDecodeWithPagedKVCacheWrapper, flashinfer_backend.py:55-58).  Split-KV over (row, KV head,
+ * page chunk) on bf16/fp16 MFMA with an fp32 online softmax.  Scale softmax_scale (1/sqrt(Dh) in the
+ * reference); query head h reads KV head h / (H / Hkv).
+ * q/out: [N, H, Dh] with element strides (tok, head), unit stride on Dh; only the rows of decode
+ * sequences are read and written.  A row with one chunk gets its output here; a row with several
+ * writes fp32 partials (m, l, acc) into the workspace, which mllm_merge_splits then combines, so the
+ * two calls go back to back on one stream.  head_dim 128, block_size a multiple of 16,
+ * H / Hkv <= 16, dtype F16 or BF16; num_merge_work (from mllm_plan) only sizes the workspace check.
+ */
+int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                      const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                      int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                      const int32_t* kv_indices, const int32_t* seq_lens, const int32_t* decode_work,
+                      int32_t num_decode_work, const int32_t* merge_work, int32_t num_merge_work,
+                      int32_t pages_per_split, float softmax_scale, int32_t dtype, void* out, int64_t out_stride_tok,
+                      int64_t out_stride_head, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Log-sum-exp merge of the split-KV partials mllm_paged_decode left in the workspace, one
+ * {seq, first_item, num_splits} merge item (mllm_plan) per row with several splits:
+ *   out = sum_j 2^(m_j - M) acc_j / sum_j 2^(m_j - M) l_j,  M = max_j m_j   (exp2 domain).
+ * This is the same combine FlashInfer's split-KV decode performs after its chunks.
+ */
+int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work, int32_t num_heads,
+                      int32_t head_dim, const int32_t* qo_indptr, int32_t dtype, void* out, int64_t out_stride_tok,
+                      int64_t out_stride_head, const void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Ragged prefill / mixed attention for rows with several new tokens (reference paged_torch_ref.py:61-73;
+ * FlashInfer BatchPrefillWithPagedKVCacheWrapper, flashinfer_backend.py:59-63): causal within each new
+ * chunk, bottom-right aligned over the cached prefix, K/V read through kv_indices.  QK^T and PV on
+ * bf16/fp16 MFMA (32x32x16) with fp32 online softmax; the H/Hkv query heads of one KV head share
+ * each K/V tile.  Work items from mllm_plan (prefill_work, q_tile_tokens = 128 / (H / Hkv)).
+ * Same shape limits as mllm_paged_decode, and H / Hkv must divide 32.
+ */
+int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                       const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* seq_lens, const int32_t* prefill_work,
+                       int32_t num_prefill_work, int32_t q_tile_tokens, float softmax_scale, int32_t dtype,
+                       void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+
+/*
+ * Contiguous causal attention, the backend's `prefill` method (reference
+ * src/minillm/attention/torch_ref.py:20-44 and base.py:19-33): q [B, H, Tq, Dh], k/v [B, Hkv, Tk, Dh]
+ * with element strides (batch, head, token) and unit stride on Dh; query i sits at position
+ * Tk - Tq + i and sees keys 0 .. Tk - Tq + i.  key_valid [B, Tk] (one byte per key, strides
+ * (batch, token), NULL for none) further limits the keys to the real ones, and a query with no real
+ * key sees its own position only.  fp32/fp16/bf16, head_dim <= 256, fp32 softmax.
+ */
+int mllm_dense_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
+                         int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                         const uint8_t* key_valid, int64_t kv_sb, int64_t kv_st, int32_t batch, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t q_len, int32_t kv_len, int32_t head_dim, float softmax_scale,
+                         int32_t dtype, void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINILLM_HIP_H */

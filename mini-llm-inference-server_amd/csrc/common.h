@@ -1,0 +1,134 @@
+// Shared helpers of the gfx950 paged-attention library: error reporting, vector types, 16-byte
+// loads/stores, bf16/fp16 conversions and the MFMA wrappers the kernels use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "minillm_hip.h"
+
+namespace mllm {
+
+// ---------------------------------------------------------------- errors
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+// Turns the last launch error (or a HIP status) into MLLM_ERR_HIP with its text.
+int check_launch(const char* what);
+
+#define MLLM_REQUIRE(cond, code, msg)        \
+  do {                                       \
+    if (!(cond)) return ::mllm::fail((code), (msg)); \
+  } while (0)
+
+// ---------------------------------------------------------------- types
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage tags: 16-bit element types are moved around as raw uint16_t bits.
+struct BF16 {};
+struct F16 {};
+
+// ---------------------------------------------------------------- conversions
+
+// float -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (what torch's .to(torch.bfloat16) gives).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  uint32_t bias = 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)((u + bias) >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+template <typename T>
+__device__ __forceinline__ uint16_t to_bits(float f);
+template <>
+__device__ __forceinline__ uint16_t to_bits<BF16>(float f) { return f32_to_bf16_bits(f); }
+template <>
+__device__ __forceinline__ uint16_t to_bits<F16>(float f) { return f32_to_f16_bits(f); }
+
+// Packs two floats into one dword of 16-bit values (lo in bits 0-15).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)to_bits<T>(lo) | ((uint32_t)to_bits<T>(hi) << 16);
+}
+
+// ---------------------------------------------------------------- memory
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Selects 16-bit halves of two dwords: returns (half `ia` of a) | (half `ib` of b) << 16.
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, int ia, uint32_t b, int ib) {
+  // v_perm_b32 selector bytes index {b: bytes 0-3, a: bytes 4-7} of the (a:b) 64-bit pair.
+  uint32_t sel_lo = ia ? 0x0706u : 0x0504u;  // half of a -> result bytes 0-1
+  uint32_t sel_hi = ib ? 0x0302u : 0x0100u;  // half of b -> result bytes 2-3
+  return __builtin_amdgcn_perm(a, b, sel_lo | (sel_hi << 16));
+}
+
+// ---------------------------------------------------------------- MFMA wrappers (gfx950)
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<BF16> {
+  // D(16x16) += A(16x32) B(32x16); lane l holds A[l%16][k-group l/16], B[k-group l/16][l%16].
+  static __device__ __forceinline__ f32x4 m16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  // D(16x16) += A(16x16) B(16x16), 4 k-values per lane.
+  static __device__ __forceinline__ f32x4 m16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c,
+                                                     0, 0, 0);
+  }
+  // D(32x32) += A(32x16) B(16x32), 8 k-values per lane.
+  static __device__ __forceinline__ f32x16 m32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<F16> {
+  static __device__ __forceinline__ f32x4 m16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+  static __device__ __forceinline__ f32x4 m16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
+  }
+  static __device__ __forceinline__ f32x16 m32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace mllm

@@ -1,0 +1,318 @@
+// Split-KV paged decode attention on gfx950 MFMA (reference src/minillm/attention/paged_torch_ref.py:47-59:
+// one new token per row, softmax(q K^T / sqrt(Dh)) V over the row's whole context).
+//
+// Work: one wavefront per (work item, KV head); a work item is a chunk of up to C pages of one row
+// (mllm_plan).  The wavefront streams its pages 16 tokens at a time straight from HBM into VGPRs:
+//   S^T[16 tok x 16] = K[16 tok x 128] . Q^T[128 x 16]      4 x v_mfma_f32_16x16x32 (bf16/f16)
+//   O^T[128 x 16]   += V^T[128 x 16 tok] . P^T[16 tok x 16]  8 x v_mfma_f32_16x16x16
+// The 16 MFMA columns hold the G = H / Hkv query heads that share the KV head (4 for Llama-3.1-8B);
+// the other columns are zero.  Because S^T and the B operand of the PV product share one lane layout
+// (lane l: column l % 16, k-rows 4 (l / 16) .. +3), P^T never leaves its lanes; the online-softmax
+// max and sum of a head are reduced across the four lanes l, l^16, l^32, l^48 that hold its column.
+// Each lane loads K row (l % 16) in four 16-byte pieces and V rows 4 (l / 16) .. +3 at dims
+// 8 (l % 16) .. +7, so every wave-wide V load reads four whole 256-byte rows; the V^T operand is then
+// assembled with v_perm_b32.  The next 16-token tile is loaded before the current one is consumed.
+// Rows with one chunk write the normalised output; longer rows write fp32 (m, l, acc) partials that a
+// second kernel merges with a log-sum-exp.
+#include <math.h>
+
+#include "common.h"
+
+namespace mllm {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kWaves = 4;  // KV heads per workgroup
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t num_blocks;
+  int bs, H, Hkv, G;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* seq_lens;
+  const int4* work;
+  int C;
+  float scale_log2;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* part_o;
+  float2* part_ml;
+};
+
+template <typename T>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, const uint16_t* kbase, const uint16_t* vbase,
+                                          int64_t tok_stride, int64_t blk_stride, int my_page, int t, int tpp, int c,
+                                          int g, u32x4 (&ka)[4], u32x4 (&va)[4]) {
+  const int page = t / tpp;
+  const int sub = t - page * tpp;
+  int blk = __builtin_amdgcn_readlane(my_page, page);
+  if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
+  const int64_t off = (int64_t)blk * blk_stride + (int64_t)(sub * 16) * tok_stride;
+  const char* kp = reinterpret_cast<const char*>(kbase + off + c * tok_stride);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ka[kk] = ld16(kp + (32 * kk + 8 * g) * 2);
+  const char* vp = reinterpret_cast<const char*>(vbase + off + (4 * g) * tok_stride + 8 * c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) va[i] = ld16(vp + (int64_t)i * tok_stride * 2);
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void decode_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int kvh = blockIdx.y * kWaves + (threadIdx.x >> 6);
+  if (kvh >= a.Hkv) return;  // wave-uniform
+  const int4 w = a.work[blockIdx.x];
+  const int seq = w.x, split = w.y, nsplit = w.z;
+  if (seq < 0) return;  // unfilled plan slot (the host pre-fills the plan with -1)
+  const int pg0 = a.kv_indptr[seq];
+  const int pgn = a.kv_indptr[seq + 1];
+  const int len = a.seq_lens[seq];
+  const int pb = pg0 + split * a.C;
+  const int pe = min(pgn, pb + a.C);
+  const int tok0 = (pb - pg0) * a.bs;
+  const int tok1 = min(len, (pe - pg0) * a.bs);
+  const int ntiles = (tok1 - tok0 + 15) >> 4;
+  const int tpp = a.bs >> 4;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int qtok = a.qo_indptr[seq];
+
+  const int my_page = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
+
+  // B operand of S^T = K Q^T: lane (c, g) holds q head c of the group at dims 32 kk + 8 g .. +7.
+  const bool qvalid = c < a.G;
+  u32x4 qf[4];
+  {
+    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qtok * a.q_st +
+                                                   (int64_t)(kvh * a.G + (qvalid ? c : 0)) * a.q_sh);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 v = ld16(qp + (32 * kk + 8 * g) * 2);
+      qf[kk] = qvalid ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+
+  const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;
+  const int64_t blk_stride = (int64_t)a.bs * tok_stride;
+  const uint16_t* kbase = a.kc + kvh * kHeadDim;
+  const uint16_t* vbase = a.vc + kvh * kHeadDim;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 ka[4], va[4];
+  load_tile<T>(a, kbase, vbase, tok_stride, blk_stride, my_page, 0, tpp, c, g, ka, va);
+  for (int t = 0; t < ntiles; ++t) {
+    u32x4 kn[4], vn[4];
+    if (t + 1 < ntiles) load_tile<T>(a, kbase, vbase, tok_stride, blk_stride, my_page, t + 1, tpp, c, g, kn, vn);
+
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) sc = Mfma<T>::m16x16x32(ka[kk], qf[kk], sc);
+
+    float s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = sc[i] * a.scale_log2;
+    const int tpos = tok0 + t * 16 + 4 * g;  // context position of this lane's first row
+    if (tok0 + t * 16 + 16 > len) {           // the row's last, partly filled tile
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (tpos + i >= len) {
+          s[i] = -INFINITY;
+          va[i] = u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_new);
+    float ps = (p[0] + p[1]) + (p[2] + p[3]);
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) o[m] *= alpha;
+
+    const u32x2 pfrag = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int dw = m >> 1, hf = m & 1;
+      const u32x2 vfrag = u32x2{pick_halves(va[0][dw], hf, va[1][dw], hf), pick_halves(va[2][dw], hf, va[3][dw], hf)};
+      o[m] = Mfma<T>::m16x16x16(vfrag, pfrag, o[m]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      ka[kk] = kn[kk];
+      va[kk] = vn[kk];
+    }
+  }
+
+  if (!qvalid) return;
+  const int head = kvh * a.G + c;
+  // lane (c, g) owns dims 32 g + 8 i + m of head c: o[m][i]
+  if (nsplit == 1) {
+    const float inv = 1.f / l_run;
+    char* op = reinterpret_cast<char*>(a.out + (int64_t)qtok * a.o_st + (int64_t)head * a.o_sh + 32 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 pk = u32x4{pack2<T>(o[0][i] * inv, o[1][i] * inv), pack2<T>(o[2][i] * inv, o[3][i] * inv),
+                       pack2<T>(o[4][i] * inv, o[5][i] * inv), pack2<T>(o[6][i] * inv, o[7][i] * inv)};
+      st16(op + 16 * i, pk);
+    }
+  } else {
+    const int64_t row = (int64_t)blockIdx.x * a.H + head;
+    float* po = a.part_o + row * kHeadDim + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<f32x4*>(po + 8 * i) = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
+      *reinterpret_cast<f32x4*>(po + 8 * i + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+    }
+    if (g == 0) a.part_ml[row] = make_float2(m_run, l_run);
+  }
+}
+
+// Log-sum-exp merge of a row's split partials: one workgroup per (row, head), one thread per dim.
+template <typename T>
+__global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict__ merge, const float* __restrict__ part_o,
+                                                         const float2* __restrict__ part_ml, int H,
+                                                         const int32_t* __restrict__ qo_indptr, uint16_t* __restrict__ out,
+                                                         int64_t o_st, int64_t o_sh) {
+  const int4 mw = merge[blockIdx.x];
+  const int seq = mw.x, first = mw.y, n = mw.z;
+  if (seq < 0) return;
+  const int head = blockIdx.y;
+  const int d = threadIdx.x;
+  float mmax = -INFINITY;
+  for (int j = 0; j < n; ++j) mmax = fmaxf(mmax, part_ml[(int64_t)(first + j) * H + head].x);
+  float lsum = 0.f, acc = 0.f;
+  for (int j = 0; j < n; ++j) {
+    const int64_t row = (int64_t)(first + j) * H + head;
+    const float2 ml = part_ml[row];
+    const float wgt = fast_exp2(ml.x - mmax);
+    lsum += wgt * ml.y;
+    acc += wgt * part_o[row * kHeadDim + d];
+  }
+  const int qtok = qo_indptr[seq];
+  out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = to_bits<T>(acc / lsum);
+}
+
+template <typename T>
+int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
+  dim3 grid(n_work, (a.Hkv + kWaves - 1) / kWaves);
+  decode_kernel<T><<<grid, 64 * kWaves, 0, st>>>(a);
+  return check_launch("mllm_paged_decode");
+}
+
+}  // namespace
+}  // namespace mllm
+
+extern "C" int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim) {
+  if (num_decode_work <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return (int64_t)num_decode_work * num_heads * ((int64_t)head_dim * 4 + 8);
+}
+
+extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                 const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                                 const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                 const int32_t* decode_work, int32_t num_decode_work, const int32_t* merge_work,
+                                 int32_t num_merge_work, int32_t pages_per_split, float softmax_scale, int32_t dtype,
+                                 void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
+               "mllm_paged_decode: dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode: head_dim must be 128");
+  MLLM_REQUIRE(block_size > 0 && block_size % 16 == 0, MLLM_ERR_UNSUPPORTED,
+               "mllm_paged_decode: block_size must be a multiple of 16");
+  MLLM_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, MLLM_ERR_INVALID,
+               "mllm_paged_decode: num_heads must be a multiple of num_kv_heads");
+  MLLM_REQUIRE(num_heads / num_kv_heads <= 16, MLLM_ERR_UNSUPPORTED,
+               "mllm_paged_decode: at most 16 query heads per KV head");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 64, MLLM_ERR_INVALID,
+               "mllm_paged_decode: pages_per_split must be in [1, 64]");
+  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID, "mllm_paged_decode: negative count");
+  if (num_decode_work == 0) return MLLM_OK;
+  MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && decode_work,
+               MLLM_ERR_INVALID, "mllm_paged_decode: null pointer");
+  const int64_t need = num_merge_work ? mllm_decode_workspace_bytes(num_decode_work, num_heads, head_dim) : 0;
+  MLLM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), MLLM_ERR_INVALID,
+               "mllm_paged_decode: workspace too small");
+  const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)out % 16 == 0) && ((uintptr_t)k_cache % 16 == 0) &&
+                       ((uintptr_t)v_cache % 16 == 0) && (q_stride_tok * 2) % 16 == 0 &&
+                       (q_stride_head * 2) % 16 == 0 && (out_stride_tok * 2) % 16 == 0 &&
+                       (out_stride_head * 2) % 16 == 0;
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode: q, out and pools need 16-byte aligned rows");
+
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.kc = static_cast<const uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.num_blocks = num_blocks;
+  a.bs = block_size;
+  a.H = num_heads;
+  a.Hkv = num_kv_heads;
+  a.G = num_heads / num_kv_heads;
+  a.qo_indptr = qo_indptr;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.seq_lens = seq_lens;
+  a.work = reinterpret_cast<const int4*>(decode_work);
+  a.C = pages_per_split;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = out_stride_tok;
+  a.o_sh = out_stride_head;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
+                                        (int64_t)num_decode_work * num_heads * head_dim * 4);
+  (void)merge_work;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MLLM_DTYPE_BF16) return launch<BF16>(a, num_decode_work, st);
+  return launch<F16>(a, num_decode_work, st);
+}
+
+extern "C" int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work,
+                                 int32_t num_heads, int32_t head_dim, const int32_t* qo_indptr, int32_t dtype,
+                                 void* out, int64_t out_stride_tok, int64_t out_stride_head, const void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
+               "mllm_merge_splits: dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, "mllm_merge_splits: head_dim must be 128");
+  MLLM_REQUIRE(num_merge_work >= 0 && num_decode_work >= 0 && num_heads > 0, MLLM_ERR_INVALID,
+               "mllm_merge_splits: bad sizes");
+  if (num_merge_work == 0) return MLLM_OK;
+  MLLM_REQUIRE(merge_work && qo_indptr && out && workspace, MLLM_ERR_INVALID, "mllm_merge_splits: null pointer");
+  MLLM_REQUIRE(workspace_bytes >= mllm_decode_workspace_bytes(num_decode_work, num_heads, head_dim), MLLM_ERR_INVALID,
+               "mllm_merge_splits: workspace too small");
+  MLLM_REQUIRE(num_heads <= 65535, MLLM_ERR_UNSUPPORTED, "mllm_merge_splits: too many heads");
+  const float* part_o = static_cast<const float*>(workspace);
+  const float2* part_ml = reinterpret_cast<const float2*>(static_cast<const char*>(workspace) +
+                                                          (int64_t)num_decode_work * num_heads * head_dim * 4);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid(num_merge_work, num_heads);
+  const int4* merge = reinterpret_cast<const int4*>(merge_work);
+  if (dtype == MLLM_DTYPE_BF16)
+    merge_kernel<BF16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                  static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+  else
+    merge_kernel<F16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                 static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+  return check_launch("mllm_merge_splits");
+}

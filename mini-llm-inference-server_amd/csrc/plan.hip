@@ -1,0 +1,102 @@
+// Per-step work plan, built on the GPU once per step and reused by every layer (the role of
+// FlashInfer's plan(), reference src/minillm/attention/flashinfer_backend.py:44-64).
+//
+// One workgroup scans the S sequences: a decode row (one new token) becomes ceil(pages / C) split-KV
+// items of C pages; a row with several new tokens becomes ceil(new / q_tile) prefill tiles, the
+// tile with the longest causal context first.  Three exclusive scans give each row its item offsets.
+#include "common.h"
+
+namespace mllm {
+namespace {
+
+constexpr int kPlanThreads = 1024;
+
+__device__ __forceinline__ int wg_exclusive_scan(int v, int* sums, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int t = __shfl_up(x, off, 64);
+    if (lane >= off) x += t;
+  }
+  if (lane == 63) sums[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < nwaves ? sums[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      int t = __shfl_up(w, off, 64);
+      if (lane >= off) w += t;
+    }
+    if (lane < nwaves) sums[lane] = w;
+  }
+  __syncthreads();
+  const int prefix = wave > 0 ? sums[wave - 1] : 0;
+  *total = sums[nwaves - 1];
+  __syncthreads();
+  return prefix + x - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ qo_indptr,
+                                                            const int32_t* __restrict__ kv_indptr, int32_t num_seqs,
+                                                            int32_t pages_per_split, int32_t q_tile,
+                                                            int4* __restrict__ decode_work, int32_t cap_decode,
+                                                            int4* __restrict__ merge_work, int32_t cap_merge,
+                                                            int2* __restrict__ prefill_work, int32_t cap_prefill) {
+  __shared__ int sums[kPlanThreads / 64];
+  int base_d = 0, base_m = 0, base_p = 0;
+  for (int base = 0; base < num_seqs; base += kPlanThreads) {
+    const int s = base + threadIdx.x;
+    int nd = 0, nm = 0, np = 0, nn = 0;
+    if (s < num_seqs) {
+      nn = qo_indptr[s + 1] - qo_indptr[s];
+      const int pages = kv_indptr[s + 1] - kv_indptr[s];
+      if (nn == 1) {
+        nd = (pages + pages_per_split - 1) / pages_per_split;
+        nm = nd > 1 ? 1 : 0;
+      } else if (nn > 1) {
+        np = (nn + q_tile - 1) / q_tile;
+      }
+    }
+    int td, tm, tp;
+    const int od = base_d + wg_exclusive_scan(nd, sums, &td);
+    const int om = base_m + wg_exclusive_scan(nm, sums, &tm);
+    const int op = base_p + wg_exclusive_scan(np, sums, &tp);
+    for (int j = 0; j < nd; ++j)
+      if (od + j < cap_decode) decode_work[od + j] = make_int4(s, j, nd, od);
+    if (nm && om < cap_merge) merge_work[om] = make_int4(s, od, nd, 0);
+    for (int j = 0; j < np; ++j)
+      if (op + j < cap_prefill) prefill_work[op + j] = make_int2(s, (np - 1 - j) * q_tile);
+    base_d += td;
+    base_m += tm;
+    base_p += tp;
+  }
+}
+
+}  // namespace
+}  // namespace mllm
+
+extern "C" int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs,
+                         int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work,
+                         int32_t num_decode_work, int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work,
+                         int32_t num_prefill_work, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, "mllm_plan: num_seqs < 0");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 64, MLLM_ERR_INVALID,
+               "mllm_plan: pages_per_split must be in [1, 64]");
+  MLLM_REQUIRE(q_tile_tokens >= 1, MLLM_ERR_INVALID, "mllm_plan: q_tile_tokens must be positive");
+  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0 && num_prefill_work >= 0, MLLM_ERR_INVALID,
+               "mllm_plan: negative capacity");
+  MLLM_REQUIRE((num_decode_work == 0 || decode_work) && (num_merge_work == 0 || merge_work) &&
+                   (num_prefill_work == 0 || prefill_work),
+               MLLM_ERR_INVALID, "mllm_plan: null work buffer");
+  if (num_seqs == 0) return MLLM_OK;
+  MLLM_REQUIRE(qo_indptr && kv_indptr, MLLM_ERR_INVALID, "mllm_plan: null indptr");
+  plan_kernel<<<1, kPlanThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      qo_indptr, kv_indptr, num_seqs, pages_per_split, q_tile_tokens, reinterpret_cast<int4*>(decode_work),
+      num_decode_work, reinterpret_cast<int4*>(merge_work), num_merge_work, reinterpret_cast<int2*>(prefill_work),
+      num_prefill_work);
+  return check_launch("mllm_plan");
+}

@@ -1,0 +1,199 @@
+"""The `hip` attention backend: minillm's paged hot path on gfx950 kernels.
+
+Drop-in for the reference's backends (src/minillm/attention/torch_ref.py:46-48,
+flashinfer_backend.py:42-64, flash_attn_backend.py:107-115): same `forward(q, k, v, k_cache, v_cache,
+meta)` and `prefill(q, k, v, key_valid)` contract, same pool layout, same metadata object.
+
+Per layer, `forward` issues on the current stream:
+1. `mllm_kv_append`     the step's k/v into the pool at `meta.slot_mapping` (bit-exact write_kv);
+2. `mllm_paged_decode`  split-KV decode for rows with one new token, then `mllm_merge_splits`;
+3. `mllm_paged_prefill` MFMA prefill for rows with several new tokens.
+A work plan (`mllm_plan`) is built on the GPU the first time a given `meta` is seen and reused by the
+other layers, like FlashInfer's plan()/run() split (flashinfer_backend.py:44).  Nothing synchronises
+the host, and there is no fallback: a missing library raises RuntimeError at construction.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+
+import torch
+
+from .. import _native
+from .base import AttentionBackend
+
+# A decode split is sized so that all splits of a step make about this many wavefronts
+# (256 CUs x 12 resident decode wavefronts x 2 rounds); clamped to [8, 64] pages.
+TARGET_DECODE_WAVES = 256 * 12 * 2
+
+
+def pages_per_split(decode_pages: int, num_kv_heads: int) -> int:
+    forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
+    if forced:
+        return max(1, min(64, int(forced)))
+    return max(8, min(64, math.ceil(decode_pages * num_kv_heads / TARGET_DECODE_WAVES)))
+
+
+@dataclass
+class StepPlan:
+    """Work lists of one step (device int32 buffers) and their sizes."""
+
+    pages_per_split: int
+    q_tile: int
+    num_decode: int
+    num_merge: int
+    num_prefill: int
+    decode_work: torch.Tensor
+    merge_work: torch.Tensor
+    prefill_work: torch.Tensor
+    workspace_bytes: int
+
+
+def _ptr(t: torch.Tensor | None) -> int:
+    return 0 if t is None or t.numel() == 0 else t.data_ptr()
+
+
+class HipBackend(AttentionBackend):
+    name = "hip"
+
+    def __init__(self) -> None:
+        self._lib = _native.lib()
+        self._planned = None  # the AttentionMetadata the plan was last built for
+        self._plan: StepPlan | None = None
+        self._workspace: torch.Tensor | None = None
+
+    # ------------------------------------------------------------------ paged path
+
+    def forward(self, q, k, v, k_cache, v_cache, meta):
+        q, k, v = self._check(q, k, v, k_cache, v_cache, meta)
+        self.append(k, v, k_cache, v_cache, meta)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        self.attend(q, k_cache, v_cache, meta, out)
+        return out
+
+    def _check(self, q, k, v, k_cache, v_cache, meta):
+        n, h, dh = q.shape
+        if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+            raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, Hkv, Dh]")
+        _, bs, hkv, dh_c = k_cache.shape
+        if k.shape != (n, hkv, dh) or v.shape != (n, hkv, dh) or dh_c != dh:
+            raise ValueError(f"k/v must be [N, Hkv, Dh] = [{n}, {hkv}, {dh}] to match q and the pool")
+        if bs != meta.block_size:
+            raise ValueError(f"pool block size {bs} != metadata block size {meta.block_size}")
+        if h % hkv:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("the KV pools must be contiguous")
+        if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+            raise ValueError("q and the pools must share one dtype")
+        if n != meta.query_start_loc[-1]:
+            raise ValueError(f"q has {n} tokens, the metadata describes {meta.query_start_loc[-1]}")
+        return tuple(t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+
+    def append(self, k, v, k_cache, v_cache, meta) -> None:
+        """KV append (reference write_kv, paged_torch_ref.py:23-28): one launch for K and V."""
+        num_blocks, bs, hkv, dh = k_cache.shape
+        self._lib.call("mllm_kv_append", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                       v.stride(1), _native.dtype_code(k.dtype), k_cache.data_ptr(), v_cache.data_ptr(),
+                       _native.dtype_code(k_cache.dtype), num_blocks * bs, hkv, dh, meta.slot_mapping.data_ptr(),
+                       k.shape[0], _native.stream_ptr(k_cache.device))
+
+    def plan(self, meta, num_heads: int, num_kv_heads: int, head_dim: int, device) -> StepPlan:
+        """The step's work plan, built on the GPU once per `meta` object and reused after."""
+        if self._planned is not meta:
+            self._make_plan(meta, num_heads, num_kv_heads, head_dim, device, _native.stream_ptr(device))
+        return self._plan
+
+    def attend(self, q, k_cache, v_cache, meta, out) -> None:
+        """Attention of every new token over its row's context in the pool, written into `out`."""
+        plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device)
+        if plan.num_decode:
+            self.run_decode(q, k_cache, v_cache, meta, out)
+            self.run_merge(q, meta, out)
+        if plan.num_prefill:
+            self.run_prefill(q, k_cache, v_cache, meta, out)
+
+    def run_decode(self, q, k_cache, v_cache, meta, out) -> None:
+        """Split-KV decode of the rows with one new token (reference paged_torch_ref.py:47-59)."""
+        plan = self._plan
+        num_blocks, bs, hkv, dh = k_cache.shape
+        ws = self._workspace_for(plan.workspace_bytes, q.device)
+        self._lib.call("mllm_paged_decode", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+                       v_cache.data_ptr(), num_blocks, bs, q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(),
+                       meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(), meta.seq_lens_i32.data_ptr(),
+                       _ptr(plan.decode_work), plan.num_decode, _ptr(plan.merge_work), plan.num_merge,
+                       plan.pages_per_split, dh ** -0.5, _native.dtype_code(k_cache.dtype), out.data_ptr(),
+                       out.stride(0), out.stride(1), _ptr(ws), plan.workspace_bytes, _native.stream_ptr(q.device))
+
+    def run_merge(self, q, meta, out) -> None:
+        """Log-sum-exp merge of the decode rows that were split."""
+        plan = self._plan
+        if not plan.num_merge:
+            return
+        self._lib.call("mllm_merge_splits", _ptr(plan.merge_work), plan.num_merge, plan.num_decode, q.shape[1],
+                       q.shape[2], meta.qo_indptr.data_ptr(), _native.dtype_code(q.dtype), out.data_ptr(),
+                       out.stride(0), out.stride(1), _ptr(self._workspace), plan.workspace_bytes,
+                       _native.stream_ptr(q.device))
+
+    def run_prefill(self, q, k_cache, v_cache, meta, out) -> None:
+        """MFMA attention of the rows with several new tokens (reference paged_torch_ref.py:61-73)."""
+        plan = self._plan
+        num_blocks, bs, hkv, dh = k_cache.shape
+        self._lib.call("mllm_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+                       v_cache.data_ptr(), num_blocks, bs, q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(),
+                       meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(), meta.seq_lens_i32.data_ptr(),
+                       _ptr(plan.prefill_work), plan.num_prefill, plan.q_tile, dh ** -0.5,
+                       _native.dtype_code(k_cache.dtype), out.data_ptr(), out.stride(0), out.stride(1),
+                       _native.stream_ptr(q.device))
+
+    def _make_plan(self, meta, h: int, hkv: int, dh: int, dev, stream: int) -> None:
+        news, lens, bs = meta.num_new, meta.seq_lens, meta.block_size
+        pages = [-(-length // bs) for length in lens]
+        decode_pages = sum(p for p, nn in zip(pages, news) if nn == 1)
+        c = pages_per_split(decode_pages, hkv)
+        g = h // hkv
+        q_tile = 128 // g if 32 % g == 0 else 1
+        n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
+        n_merge = sum(1 for p, nn in zip(pages, news) if nn == 1 and p > c)
+        n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
+        buf = torch.full((4 * n_dec + 4 * n_merge + 2 * n_pf,), -1, dtype=torch.int32, device=dev)
+        dec, mrg, pf = buf[:4 * n_dec], buf[4 * n_dec:4 * (n_dec + n_merge)], buf[4 * (n_dec + n_merge):]
+        self._lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs, c, q_tile,
+                       _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf, stream)
+        ws = self._lib.workspace_bytes(n_dec, h, dh) if n_merge else 0
+        self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws)
+        self._planned = meta
+
+    def _workspace_for(self, nbytes: int, dev) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        if self._workspace is None or self._workspace.numel() < nbytes or self._workspace.device != dev:
+            self._workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        return self._workspace
+
+    # ------------------------------------------------------------------ contiguous path
+
+    def prefill(self, q, k, v, key_valid=None, **kwargs):
+        b, h, tq, dh = q.shape
+        bk, hkv, tk, dhk = k.shape
+        if v.shape != k.shape or bk != b or dhk != dh:
+            raise ValueError("k and v must be [B, Hkv, Tk, Dh] matching q [B, H, Tq, Dh]")
+        if tk < tq:
+            raise ValueError("Tk must be >= Tq")
+        if not (q.dtype == k.dtype == v.dtype):
+            raise ValueError("q, k and v must share one dtype")
+        q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+        out = torch.empty((b, h, tq, dh), dtype=q.dtype, device=q.device)
+        kv_ptr, kv_sb, kv_st = 0, 0, 0
+        if key_valid is not None:
+            if key_valid.shape != (b, tk):
+                raise ValueError(f"key_valid must be [B, Tk] = [{b}, {tk}]")
+            key_valid = key_valid.to(device=q.device, dtype=torch.bool).contiguous().view(torch.uint8)
+            kv_ptr, kv_sb, kv_st = key_valid.data_ptr(), key_valid.stride(0), key_valid.stride(1)
+        self._lib.call("mllm_dense_attention", q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(),
+                       k.stride(0), k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+                       kv_ptr, kv_sb, kv_st, b, h, hkv, tq, tk, dh, dh ** -0.5, _native.dtype_code(q.dtype),
+                       out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _native.stream_ptr(q.device))
+        return out

@@ -1,0 +1,117 @@
+"""Oracle: the torch reference attention, restated.  TEST INFRASTRUCTURE ONLY.
+
+Follows reference `src/minillm/attention/paged_torch_ref.py:23-74` and
+`src/minillm/attention/torch_ref.py:20-48` step for step, calling the same torch library routines
+(`index_copy_`, advanced-index gather, `F.scaled_dot_product_attention` with `enable_gqa=True`) on the
+same shapes, so that its rounding is the reference's own:
+
+- decode rows (one new token) are attended together, gathered to the longest context and masked
+  past each row's length (`paged_torch_ref.py:47-59`);
+- rows with several new tokens run one at a time, `is_causal=True` when the row is a fresh prompt and
+  a bottom-right aligned `tril(length - n)` mask otherwise (`paged_torch_ref.py:61-73`).
+
+Runs on any torch device.  On a GPU, callers pass float32 tensors (the bf16 batched-matmul path of
+torch is avoided there); on the CPU it runs in the caller's dtype, exactly as the reference does.
+"""
+
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace
+
+import torch
+import torch.nn.functional as F
+
+from .metadata import OracleMetadata
+
+
+def torch_meta(meta: OracleMetadata, device) -> SimpleNamespace:
+    """The host lists plus the int64 block table on `device`: all `paged_attention` reads."""
+    return SimpleNamespace(
+        query_start_loc=list(meta.query_start_loc),
+        seq_lens=list(meta.seq_lens),
+        num_new=meta.num_new,
+        block_tables=torch.as_tensor(meta.block_tables, dtype=torch.long, device=device),
+        slot_mapping=torch.as_tensor(meta.slot_mapping, dtype=torch.long, device=device),
+    )
+
+
+def write_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch.Tensor,
+             v: torch.Tensor) -> None:
+    """Reference `paged_torch_ref.py:23-28`: k, v [N, Hkv, Dh] scattered into the flat pool view at
+    `slot_mapping` [N] (int64), after a cast to the pool's dtype."""
+    hkv, dh = k_cache.shape[-2:]
+    k_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, k.to(k_cache.dtype))
+    v_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, v.to(v_cache.dtype))
+
+
+def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torch.Tensor:
+    """Reference `paged_torch_ref.py:31-37`: [num_blocks, bs, Hkv, Dh] through tables [B, nb] ->
+    [B, Hkv, length, Dh], the first `length` tokens of every row."""
+    b = block_tables.shape[0]
+    bs, hkv, dh = cache.shape[1:]
+    nb = math.ceil(length / bs)
+    tokens = cache[block_tables[:, :nb]].reshape(b, nb * bs, hkv, dh)[:, :length]
+    return tokens.transpose(1, 2)
+
+
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta) -> torch.Tensor:
+    """Reference `paged_torch_ref.py:40-74`.  q [N, H, Dh] -> [N, H, Dh]; the step's own k/v must
+    already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`."""
+    out = torch.empty_like(q)
+    starts, lens, news = meta.query_start_loc, meta.seq_lens, meta.num_new
+
+    decode = [i for i, n in enumerate(news) if n == 1]
+    if decode:
+        rows = torch.tensor(decode, device=q.device)
+        longest = max(lens[i] for i in decode)
+        k = gather(k_cache, meta.block_tables[rows], longest)
+        v = gather(v_cache, meta.block_tables[rows], longest)
+        token_idx = torch.tensor([starts[i] for i in decode], device=q.device)
+        qd = q[token_idx][:, :, None]
+        mask = None
+        if any(lens[i] != longest for i in decode):
+            ends = torch.tensor([lens[i] for i in decode], device=q.device)
+            mask = (torch.arange(longest, device=q.device)[None, :] < ends[:, None])[:, None, None, :]
+        out[token_idx] = F.scaled_dot_product_attention(qd, k, v, attn_mask=mask, enable_gqa=True)[:, :, 0]
+
+    for i, n in enumerate(news):
+        if n == 1:
+            continue
+        s, length = starts[i], lens[i]
+        k = gather(k_cache, meta.block_tables[i:i + 1], length)
+        v = gather(v_cache, meta.block_tables[i:i + 1], length)
+        qi = q[s:s + n].transpose(0, 1)[None]
+        if n == length:
+            o = F.scaled_dot_product_attention(qi, k, v, is_causal=True, enable_gqa=True)
+        else:
+            mask = torch.ones(n, length, dtype=torch.bool, device=q.device).tril(diagonal=length - n)
+            o = F.scaled_dot_product_attention(qi, k, v, attn_mask=mask, enable_gqa=True)
+        out[s:s + n] = o[0].transpose(0, 1)
+    return out
+
+
+def forward(q, k, v, k_cache, v_cache, meta) -> torch.Tensor:
+    """Reference `torch_ref.py:46-48`: write the step's k/v into the pool, then attend."""
+    write_kv(k_cache, v_cache, meta.slot_mapping, k, v)
+    return paged_attention(q, k_cache, v_cache, meta)
+
+
+def prefill(q, k, v, key_valid=None) -> torch.Tensor:
+    """Reference `torch_ref.py:20-44`: contiguous attention.  q [B, H, Tq, Dh], k/v [B, Hkv, Tk, Dh];
+    the queries are the last Tq of the Tk positions.  With `key_valid` [B, Tk] (bool) the mask is
+    bottom-right causal AND key-is-real, and a query with no real key may see its own position."""
+    tq, tk = q.shape[2], k.shape[2]
+    if key_valid is not None:
+        causal = torch.ones(tq, tk, dtype=torch.bool, device=q.device).tril(diagonal=tk - tq)
+        mask = causal & key_valid[:, None, None, :]
+        own = torch.zeros(tq, tk, dtype=torch.bool, device=q.device)
+        own[torch.arange(tq), torch.arange(tq) + tk - tq] = True
+        mask = mask | (own & ~mask.any(dim=-1, keepdim=True))
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
+    if tq == tk:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+    if tq == 1:
+        return F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    mask = torch.ones(tq, tk, dtype=torch.bool, device=q.device).tril(diagonal=tk - tq)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)

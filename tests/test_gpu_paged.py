@@ -1,0 +1,267 @@
+"""GPU parity of the HIP paged path against the oracle, on identical seeded inputs.
+
+- metadata: every tensor field bit-identical (value and dtype) to the oracle's build, plus host lists;
+- KV append: the pool bit-identical to the oracle's write_kv;
+- attention: within 2e-2 abs / 1e-2 rel of the oracle's gather + SDPA computed in float32;
+- junk in pool slots a row does not own never changes a bit of the output.
+The oracle runs on the same GPU in float32 (torch's bf16 batched matmul is not used).
+"""
+
+import json
+import random
+from pathlib import Path
+
+import pytest
+import torch
+
+from harness import ATOL, RTOL, bits, hip_step, oracle_step
+from oracle.metadata import OracleSeq, build_metadata
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _meta_fields_equal(meta, om):
+    assert meta.query_start_loc == om.query_start_loc
+    assert meta.seq_lens == om.seq_lens
+    for name in om.TENSOR_FIELDS:
+        got = getattr(meta, name)
+        exp = torch.from_numpy(getattr(om, name))
+        assert got.dtype == exp.dtype, name
+        assert got.shape == exp.shape, name
+        assert torch.equal(got.cpu(), exp), name
+
+
+# ------------------------------------------------------------------ metadata
+
+
+def test_metadata_known_answer(hip):
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    g = json.loads((GOLDEN / "metadata_kat.json").read_text())
+    meta = AttentionMetadata.build([SeqStep(c, n, b) for c, n, b in g["seqs"]], g["block_size"], DEV)
+    for name, exp in g["expected"].items():
+        got = getattr(meta, name)
+        got = got if isinstance(got, list) else got.cpu().tolist()
+        assert got == exp, name
+    for name, dt in g["dtypes"].items():
+        assert str(getattr(meta, name).dtype) == f"torch.{dt}", name
+
+
+@pytest.mark.parametrize("bs", [1, 4, 16, 32])
+@pytest.mark.parametrize("seed", range(3))
+def test_metadata_random_steps(hip, bs, seed):
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    rng = random.Random(seed)
+    perm = list(range(200000))
+    rng.shuffle(perm)
+    seqs, o = [], 0
+    for _ in range(rng.randrange(1, 1500)):
+        cached = rng.choice([0, rng.randrange(0, 3000)])
+        new = rng.choice([1, 1, 1, rng.randrange(1, 300)])
+        need = -(-(cached + new) // bs) + rng.randrange(0, 3)
+        seqs.append((cached, new, perm[o:o + need]))
+        o += need
+    meta = AttentionMetadata.build([SeqStep(*s) for s in seqs], bs, DEV)
+    _meta_fields_equal(meta, build_metadata([OracleSeq(*s) for s in seqs], bs))
+
+
+@pytest.mark.parametrize("name", ["decode_4", "decode_256", "mixed_128", "prefix_64"])
+def test_metadata_workloads(hip, name):
+    from minillm import workloads
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    wl = workloads.WORKLOADS[name]()
+    meta = AttentionMetadata.build([SeqStep(*s) for s in wl.seqs], wl.block_size, DEV)
+    _meta_fields_equal(meta, build_metadata([OracleSeq(*s) for s in wl.seqs], wl.block_size))
+
+
+# ------------------------------------------------------------------ append + attention on the workloads
+
+
+@pytest.mark.parametrize("name", ["decode_4", "decode_256", "mixed_128", "prefix_64"])
+def test_workload_parity(hip, name):
+    from minillm import workloads
+
+    wl = workloads.WORKLOADS[name]()
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_fp16_pool_parity(hip):
+    from minillm import workloads
+
+    wl = workloads.mixed_128(dtype=torch.float16)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def _junk(value):
+    def fill(pk, pv, wl):
+        used = torch.zeros(wl.num_blocks * wl.block_size, dtype=torch.bool)
+        for c, n, blocks in wl.seqs:
+            for p in range(c):  # cached context stays; everything else becomes junk
+                used[blocks[p // wl.block_size] * wl.block_size + p % wl.block_size] = True
+        junk = ~used.to(pk.device)
+        if value == "nan":
+            pk.view(-1, wl.hkv, wl.dh)[junk] = float("nan")
+            pv.view(-1, wl.hkv, wl.dh)[junk] = float("nan")
+        else:
+            pk.view(-1, wl.hkv, wl.dh)[junk] = value
+            pv.view(-1, wl.hkv, wl.dh)[junk] = value
+    return fill
+
+
+@pytest.mark.parametrize("name", ["decode_4", "mixed_128"])
+def test_slots_a_row_does_not_own_never_matter(hip, name):
+    # reference tests/test_paged.py:104-106 fills the pool with 1e4; NaN junk is stricter still
+    from minillm import workloads
+
+    wl = workloads.WORKLOADS[name]()
+    outs = [hip_step(wl, DEV, pool_fill=_junk(v))[0] for v in (0.0, 1e4, "nan")]
+    assert torch.equal(bits(outs[0]), bits(outs[1])) and torch.equal(bits(outs[0]), bits(outs[2]))
+
+
+# ------------------------------------------------------------------ the reference's own kernel harness
+
+
+def _kernel_case(h=8, hkv=2, dh=128, bs=16, dtype=torch.bfloat16, steps=None, seed=0, num_blocks=64):
+    """tests/test_kernels.py:29-48 of the reference: a ragged step with every row kind over a
+    random-junk pool and shuffled blocks."""
+    from minillm.workloads import Workload
+
+    g = torch.Generator().manual_seed(seed)
+    steps = steps or [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1)]
+    pool_k = torch.randn(num_blocks, bs, hkv, dh, generator=g).to(dtype)
+    pool_v = torch.randn(num_blocks, bs, hkv, dh, generator=g).to(dtype)
+    free = list(range(num_blocks))
+    random.Random(3).shuffle(free)
+    seqs = []
+    for cached, new in steps:
+        n = cached + new
+        seqs.append((cached, new, [free.pop() for _ in range(-(-n // bs))]))
+    n = sum(new for _, new in steps)
+    q = torch.randn(n, h, dh, generator=g).to(dtype)
+    k = torch.randn(n, hkv, dh, generator=g).to(dtype)
+    v = torch.randn(n, hkv, dh, generator=g).to(dtype)
+    return Workload("kernel_case", seqs, num_blocks, q, k, v, pool_k, pool_v, h=h, hkv=hkv, dh=dh, block_size=bs)
+
+
+def test_reference_mixed_step(hip):
+    wl = _kernel_case()
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))  # identical writes
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_reference_decode_only_step(hip):
+    # tests/test_kernels.py:62-72: contexts 5 / 63 / 17, 4-block tables (wider than needed)
+    wl = _kernel_case(steps=[(5, 1), (63, 1), (17, 1)])
+    wl.seqs = [(c, n, list(range(i * 4, i * 4 + 4))) for i, (c, n, _) in enumerate(wl.seqs)]
+    out, *_ = hip_step(wl, DEV)
+    ref, *_ = oracle_step(wl, DEV)
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("h,hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (32, 1)], ids=["g1", "g2", "g8", "g16", "g32"])
+def test_group_sizes(hip, h, hkv):
+    steps = [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (17, 70)]
+    wl = _kernel_case(h=h, hkv=hkv, steps=steps)
+    if h // hkv > 16:  # decode supports up to 16 query heads per KV head
+        wl.seqs = [s for s in wl.seqs]
+        with pytest.raises(ValueError, match="16 query heads"):
+            hip_step(wl, DEV)
+        return
+    out, *_ = hip_step(wl, DEV)
+    ref, *_ = oracle_step(wl, DEV)
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_larger_blocks(hip, bs):
+    wl = _kernel_case(bs=bs, steps=[(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (129, 130)], num_blocks=48)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_llama_call_site_views(hip):
+    # the model passes q[0].transpose(0, 1) of a [1, H, N, Dh] tensor: token stride Dh, head stride N*Dh
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    wl = _kernel_case(h=32, hkv=8)
+    n = wl.num_tokens
+    q4 = wl.q.transpose(0, 1).contiguous()[None]  # [1, H, N, Dh]
+    k4 = wl.k.transpose(0, 1).contiguous()[None]
+    v4 = wl.v.transpose(0, 1).contiguous()[None]
+    meta = AttentionMetadata.build([SeqStep(*s) for s in wl.seqs], wl.block_size, DEV)
+    pk, pv = wl.pool_k.to(DEV), wl.pool_v.to(DEV)
+    qd, kd, vd = (t.to(DEV)[0].transpose(0, 1) for t in (q4, k4, v4))
+    assert not qd.is_contiguous() and qd.shape == (n, 32, 128)
+    out = get_backend("hip").forward(qd, kd, vd, pk, pv, meta)
+    ref, rk, _ = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_plan_is_reused_per_metadata(hip):
+    from minillm.attention import get_backend
+
+    wl = _kernel_case()
+    backend = get_backend("hip")
+    out1, pk, pv, meta = hip_step(wl, DEV, backend=backend)
+    plan = backend._plan
+    out2 = backend.forward(wl.q.to(DEV), wl.k.to(DEV), wl.v.to(DEV), pk, pv, meta)
+    assert backend._plan is plan  # same metadata object: no re-plan (the 32-layer reuse)
+    assert torch.equal(bits(out1), bits(out2))
+
+
+def test_plan_contents(hip):
+    # the GPU plan against the split rule it implements, on rows of many lengths
+    from minillm.attention.hip_backend import HipBackend
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    rng = random.Random(7)
+    steps = [(rng.randrange(0, 5000), rng.choice([1, 1, 2, 40, 200])) for _ in range(300)]
+    seqs, o = [], 0
+    for c, n in steps:
+        need = -(-(c + n) // 16)
+        seqs.append(SeqStep(c, n, list(range(o, o + need))))
+        o += need
+    meta = AttentionMetadata.build(seqs, 16, DEV)
+    backend = HipBackend()
+    backend._make_plan(meta, 32, 8, 128, torch.device(DEV), torch.cuda.current_stream().cuda_stream)
+    p = backend._plan
+    c = p.pages_per_split
+    dec = p.decode_work.view(-1, 4).cpu().tolist()
+    exp_dec, exp_merge, exp_pf = [], [], []
+    for s, (cached, n) in enumerate(steps):
+        pages = -(-(cached + n) // 16)
+        if n == 1:
+            ns = -(-pages // c)
+            first = len(exp_dec)
+            exp_dec += [[s, j, ns, first] for j in range(ns)]
+            if ns > 1:
+                exp_merge.append([s, first, ns, 0])
+        else:
+            nt = -(-n // p.q_tile)
+            exp_pf += [[s, (nt - 1 - j) * p.q_tile] for j in range(nt)]
+    assert dec == exp_dec
+    assert p.merge_work.view(-1, 4).cpu().tolist() == exp_merge
+    assert p.prefill_work.view(-1, 2).cpu().tolist() == exp_pf
+
+
+def test_unsupported_shapes_raise(hip):
+    wl = _kernel_case(dh=64)
+    with pytest.raises(ValueError, match="head_dim"):
+        hip_step(wl, DEV)

@@ -1,0 +1,115 @@
+"""CPU-only checks of the host side: the C ABI library loads and exports exactly what
+include/minillm_hip.h declares, the Python bindings cover the same list, and the host logic raises
+the reference's errors.  No kernel is launched here."""
+
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "minillm_hip.h"
+PKG = ROOT / "mini-llm-inference-server_amd"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(mllm_[a-z0-9_]+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def libpath():
+    from minillm import _native
+
+    if not _native.LIB_PATH.exists():  # nothing built yet: build it (this is the build check, not a fallback)
+        sys.path.insert(0, str(PKG))
+        import build_hip
+
+        build_hip.build()
+    return _native.LIB_PATH
+
+
+def test_header_declares_the_abi():
+    syms = declared_symbols()
+    assert {"mllm_last_error", "mllm_build_metadata", "mllm_kv_append", "mllm_plan", "mllm_paged_decode",
+            "mllm_merge_splits", "mllm_paged_prefill", "mllm_dense_attention",
+            "mllm_decode_workspace_bytes", "mllm_abi_version"} <= syms
+
+
+def test_library_exports_every_declared_symbol(libpath):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(libpath)], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\b(mllm_[a-z0-9_]+)\b", out.stdout))
+    assert declared_symbols() == exported
+
+
+def test_bindings_cover_the_header(libpath):
+    from minillm import _native
+
+    assert set(_native.SIGNATURES) == declared_symbols()
+    lib = _native.lib()  # loads without a GPU; checks the ABI version
+    assert lib.last_error() == ""
+    assert lib.workspace_bytes(10, 32, 128) == 10 * 32 * (128 * 4 + 8)
+    assert lib.workspace_bytes(0, 32, 128) == 0
+
+
+def test_argument_errors_map_to_value_error(libpath):
+    from minillm import _native
+
+    lib = _native.lib()
+    with pytest.raises(ValueError, match="pages_per_split"):
+        lib.call("mllm_plan", 0, 0, 1, 0, 32, 0, 0, 0, 0, 0, 0, 0)
+    with pytest.raises(ValueError, match="head_dim"):
+        lib.call("mllm_paged_decode", 0, 0, 0, 0, 0, 0, 16, 32, 8, 64, 0, 0, 0, 0, 0, 1, 0, 0, 8, 1.0, 2, 0, 0, 0, 0,
+                 0, 0)
+    with pytest.raises(ValueError, match="dtype"):
+        lib.call("mllm_paged_prefill", 0, 0, 0, 0, 0, 0, 16, 32, 8, 128, 0, 0, 0, 0, 0, 1, 32, 1.0, 0, 0, 0, 0, 0)
+    with pytest.raises(ValueError, match="divide 32"):
+        lib.call("mllm_paged_prefill", 0, 0, 0, 0, 0, 0, 16, 24, 8, 128, 0, 0, 0, 0, 0, 1, 32, 1.0, 2, 0, 0, 0, 0)
+    assert "divide 32" in lib.last_error()
+    # zero-sized work is a no-op that launches nothing
+    lib.call("mllm_kv_append", 0, 0, 0, 0, 0, 0, 2, 0, 0, 2, 0, 8, 128, 0, 0, 0)
+    lib.call("mllm_paged_decode", 0, 0, 0, 0, 0, 0, 16, 32, 8, 128, 0, 0, 0, 0, 0, 0, 0, 0, 8, 1.0, 2, 0, 0, 0, 0, 0, 0)
+
+
+def test_registry():
+    from minillm.attention import get_backend
+
+    with pytest.raises(ValueError, match="unknown attention backend"):
+        get_backend("torch_ref_typo")
+
+
+def test_metadata_short_table_raises_before_touching_a_device():
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    with pytest.raises(ValueError, match="can't hold"):
+        AttentionMetadata.build([SeqStep(0, 5, [2])], 4, "cpu")
+    with pytest.raises(RuntimeError, match="GPU"):
+        AttentionMetadata.build([SeqStep(3, 1, [7])], 4, "cpu")
+
+
+def test_split_size_heuristic(monkeypatch):
+    from minillm.attention import hip_backend
+
+    monkeypatch.delenv("MLLM_PAGES_PER_SPLIT", raising=False)
+    assert hip_backend.pages_per_split(10, 8) == 8
+    assert hip_backend.pages_per_split(10 ** 7, 8) == 64
+    c = hip_backend.pages_per_split(34000, 8)
+    assert 8 <= c <= 64
+    monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", "5")
+    assert hip_backend.pages_per_split(34000, 8) == 5
+
+
+def test_workloads_are_deterministic_and_sized():
+    from minillm import workloads
+
+    a, b = workloads.decode_4(), workloads.decode_4()
+    assert torch.equal(a.q, b.q) and a.seqs == b.seqs
+    assert [c for c, _, _ in a.seqs] == [37, 128, 211, 500]
+    assert [len(t) for _, _, t in a.seqs] == [3, 9, 14, 32]
+    assert a.algorithmic_bytes() == 3_604_480 + 65_536 + 32_768 + 232 + 4 * 13
+    used = [b for _, _, t in a.seqs for b in t]
+    assert len(set(used)) == len(used) and max(used) < a.num_blocks

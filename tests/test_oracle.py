@@ -1,0 +1,252 @@
+"""Pins the CPU oracle against the reference's own known answers and against the mathematics.
+
+Nothing here compares the oracle with a retyped copy of itself: metadata is checked against the
+reference's KAT and against per-token/per-page invariants; attention against float64 textbook
+attention written with explicit per-head loops (tests/naive.py).
+"""
+
+import json
+import math
+import random
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from naive import causal_allowed, dense_context, naive_attention
+from oracle import torch_ref
+from oracle.metadata import OracleSeq, build_metadata
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def kat():
+    return json.loads((GOLDEN / "metadata_kat.json").read_text())
+
+
+# ---------------------------------------------------------------- metadata
+
+
+def test_metadata_known_answer():
+    g = kat()
+    meta = build_metadata([OracleSeq(c, n, b) for c, n, b in g["seqs"]], g["block_size"])
+    exp = g["expected"]
+    assert meta.query_start_loc == exp["query_start_loc"]
+    assert meta.seq_lens == exp["seq_lens"]
+    assert meta.num_new == exp["num_new"]
+    for name, dt in g["dtypes"].items():
+        arr = getattr(meta, name)
+        assert arr.dtype == np.dtype(dt), name
+        assert arr.tolist() == exp[name], name
+
+
+def test_metadata_short_table_raises():
+    g = kat()["short_table"]
+    with pytest.raises(ValueError, match=g["error"]):
+        build_metadata([OracleSeq(c, n, b) for c, n, b in g["seqs"]], g["block_size"])
+
+
+def random_steps(rng, count, bs, max_ctx=300, slack=2):
+    seqs = []
+    used = set()
+    nxt = 0
+    perm = list(range(100000))
+    rng.shuffle(perm)
+    for _ in range(count):
+        cached = rng.choice([0, rng.randrange(0, max_ctx)])
+        new = rng.choice([1, 1, rng.randrange(1, 70)])
+        need = -(-(cached + new) // bs) + rng.randrange(0, slack + 1)  # tables may be wider than needed
+        blocks = perm[nxt:nxt + need]
+        nxt += need
+        used.update(blocks)
+        seqs.append(OracleSeq(cached, new, blocks))
+    return seqs
+
+
+@pytest.mark.parametrize("bs", [1, 4, 16])
+@pytest.mark.parametrize("seed", range(4))
+def test_metadata_invariants(bs, seed):
+    rng = random.Random(seed)
+    seqs = random_steps(rng, rng.randrange(1, 40), bs)
+    meta = build_metadata(seqs, bs)
+    starts = meta.query_start_loc
+    assert starts[0] == 0 and all(starts[i + 1] - starts[i] == s.num_new for i, s in enumerate(seqs))
+    assert meta.qo_indptr.tolist() == starts
+    assert meta.seq_lens == [s.num_cached + s.num_new for s in seqs] == meta.seq_lens_i32.tolist()
+    width = max(len(s.block_ids) for s in seqs)
+    assert meta.block_tables.shape == (len(seqs), width)
+    for i, s in enumerate(seqs):
+        row = meta.block_tables[i].tolist()
+        assert row[:len(s.block_ids)] == s.block_ids and all(b == 0 for b in row[len(s.block_ids):])
+        # every new token: position = cached + offset, slot decodes to (table[pos // bs], pos % bs)
+        for j in range(s.num_new):
+            t = starts[i] + j
+            pos = int(meta.positions[t])
+            slot = int(meta.slot_mapping[t])
+            assert pos == s.num_cached + j
+            assert slot // bs == s.block_ids[pos // bs] and slot % bs == pos % bs
+        # pages: a prefix of the table, exactly enough blocks for the context
+        lo, hi = int(meta.kv_indptr[i]), int(meta.kv_indptr[i + 1])
+        length = meta.seq_lens[i]
+        assert (hi - lo - 1) * bs < length <= (hi - lo) * bs
+        assert meta.kv_indices[lo:hi].tolist() == s.block_ids[:hi - lo]
+        last = int(meta.kv_last_page_len[i])
+        assert 1 <= last <= bs and (hi - lo - 1) * bs + last == length
+        assert int(meta.logits_index[i]) == starts[i + 1] - 1
+    assert int(meta.kv_indptr[-1]) == meta.kv_indices.size
+    assert np.array_equal(meta.block_tables_i32, meta.block_tables.astype(np.int32))
+
+
+# ---------------------------------------------------------------- write_kv / gather
+
+
+def test_write_then_gather_round_trip():
+    # reference tests/test_paged.py:53-60
+    pool = torch.zeros(6, 4, 2, 3)
+    other = torch.zeros_like(pool)
+    k = torch.randn(7, 2, 3)
+    slots = torch.tensor([5 * 4 + i for i in range(4)] + [1 * 4 + i for i in range(3)])
+    torch_ref.write_kv(pool, other, slots, k, k)
+    got = torch_ref.gather(pool, torch.tensor([[5, 1]]), 7)
+    torch.testing.assert_close(got[0].transpose(0, 1), k)
+
+
+def test_write_touches_only_its_slots():
+    g = torch.Generator().manual_seed(5)
+    pool_k = torch.randn(10, 4, 2, 8, generator=g)
+    pool_v = torch.randn(10, 4, 2, 8, generator=g)
+    before_k, before_v = pool_k.clone(), pool_v.clone()
+    slots = torch.tensor([3, 17, 38, 0])
+    k, v = torch.randn(4, 2, 8, generator=g), torch.randn(4, 2, 8, generator=g)
+    torch_ref.write_kv(pool_k, pool_v, slots, k, v)
+    flat_k, flat_v = pool_k.view(-1, 2, 8), pool_v.view(-1, 2, 8)
+    assert torch.equal(flat_k[slots], k) and torch.equal(flat_v[slots], v)
+    keep = torch.ones(40, dtype=torch.bool)
+    keep[slots] = False
+    assert torch.equal(flat_k[keep], before_k.view(-1, 2, 8)[keep])
+    assert torch.equal(flat_v[keep], before_v.view(-1, 2, 8)[keep])
+
+
+# ---------------------------------------------------------------- paged attention
+
+
+def build_step(case, dtype=torch.float32, junk=None):
+    """The reference's paged == dense harness (tests/test_paged.py:63-93): earlier tokens are already
+    in the pool, this step's are passed in."""
+    torch.manual_seed(case["torch_seed"])
+    h, hkv, dh, bs, nb = case["h"], case["hkv"], case["dh"], case["bs"], case["num_blocks"]
+    pool_k = torch.zeros(nb, bs, hkv, dh, dtype=dtype)
+    pool_v = torch.zeros(nb, bs, hkv, dh, dtype=dtype)
+    if junk is not None:
+        pool_k.fill_(junk)
+        pool_v.fill_(junk)
+    free = list(range(nb))
+    random.Random(case["shuffle_seed"]).shuffle(free)
+    seqs, ctx_k, ctx_v = [], [], []
+    for cached, new in case["steps"]:
+        n = cached + new
+        blocks = [free.pop() for _ in range(-(-n // bs))]
+        k, v = torch.randn(n, hkv, dh).to(dtype), torch.randn(n, hkv, dh).to(dtype)
+        if cached:
+            slots = torch.tensor([blocks[p // bs] * bs + p % bs for p in range(cached)])
+            torch_ref.write_kv(pool_k, pool_v, slots, k[:cached], v[:cached])
+        seqs.append(OracleSeq(cached, new, blocks))
+        ctx_k.append(k)
+        ctx_v.append(v)
+    meta = build_metadata(seqs, bs)
+    q = torch.randn(sum(new for _, new in case["steps"]), h, dh).to(dtype)
+    new_k = torch.cat([k[c:] for k, (c, _) in zip(ctx_k, case["steps"])])
+    new_v = torch.cat([v[c:] for v, (c, _) in zip(ctx_v, case["steps"])])
+    return q, new_k, new_v, pool_k, pool_v, meta, seqs, ctx_k, ctx_v
+
+
+def cases():
+    return json.loads((GOLDEN / "cases.json").read_text())
+
+
+def test_paged_attention_equals_textbook():
+    case = cases()["paged_equals_dense"]
+    q, k, v, pool_k, pool_v, meta, seqs, ctx_k, ctx_v = build_step(case)
+    out = torch_ref.forward(q, k, v, pool_k, pool_v, torch_ref.torch_meta(meta, "cpu"))
+    for i, s in enumerate(seqs):
+        st, n, length = meta.query_start_loc[i], s.num_new, meta.seq_lens[i]
+        exp = naive_attention(q[st:st + n].transpose(0, 1), ctx_k[i].transpose(0, 1), ctx_v[i].transpose(0, 1),
+                              causal_allowed(n, length))
+        torch.testing.assert_close(out[st:st + n].double(), exp.transpose(0, 1), atol=1e-5, rtol=1e-5)
+        # and the pool really holds the context at the table's slots
+        assert torch.equal(dense_context(pool_k, s.block_ids, length), ctx_k[i].transpose(0, 1))
+
+
+def test_paged_attention_ignores_slots_it_does_not_own():
+    case = cases()["paged_equals_dense"]
+    outs = []
+    for junk in (None, 1e4):
+        q, k, v, pool_k, pool_v, meta, *_ = build_step(case, junk=junk)
+        outs.append(torch_ref.forward(q, k, v, pool_k, pool_v, torch_ref.torch_meta(meta, "cpu")))
+    torch.testing.assert_close(outs[0], outs[1], atol=1e-6, rtol=1e-6)
+
+
+def test_paged_attention_bf16_kernel_case_close_to_textbook():
+    # the reference's kernel harness shapes (tests/test_kernels.py:29-48) run on the CPU oracle in bf16
+    case = cases()["kernel_mixed_step"]
+    q, k, v, pool_k, pool_v, meta, seqs, ctx_k, ctx_v = build_step(case, dtype=torch.bfloat16)
+    out = torch_ref.forward(q, k, v, pool_k, pool_v, torch_ref.torch_meta(meta, "cpu"))
+    for i, s in enumerate(seqs):
+        st, n, length = meta.query_start_loc[i], s.num_new, meta.seq_lens[i]
+        exp = naive_attention(q[st:st + n].transpose(0, 1), ctx_k[i].transpose(0, 1), ctx_v[i].transpose(0, 1),
+                              causal_allowed(n, length))
+        torch.testing.assert_close(out[st:st + n].double(), exp.transpose(0, 1), atol=2e-2, rtol=1e-2)
+
+
+# ---------------------------------------------------------------- contiguous prefill
+
+
+def naive_dense(q, k, v, allowed):
+    return torch.stack([naive_attention(q[b], k[b], v[b], allowed[b]) for b in range(q.shape[0])])
+
+
+@pytest.mark.parametrize("h,hkv", [(4, 4), (4, 2), (8, 1)], ids=["mha", "gqa", "mqa"])
+def test_prefill_matches_textbook(h, hkv):
+    # reference tests/test_attention.py:22-30
+    g = torch.Generator().manual_seed(0)
+    b, t, dh = 2, 7, 16
+    q, k, v = (torch.randn(b, n, t, dh, generator=g) for n in (h, hkv, hkv))
+    out = torch_ref.prefill(q, k, v)
+    allowed = causal_allowed(t, t)[None].expand(b, t, t)
+    torch.testing.assert_close(out.double(), naive_dense(q, k, v, allowed), atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("tq,tk", [(1, 9), (4, 9), (9, 9)], ids=["decode", "continue", "fresh"])
+def test_prefill_on_top_of_cache(tq, tk):
+    # reference tests/test_attention.py:47-55
+    g = torch.Generator().manual_seed(2)
+    q_all, k, v = (torch.randn(1, n, tk, 16, generator=g) for n in (4, 2, 2))
+    q = q_all[:, :, -tq:]
+    out = torch_ref.prefill(q, k, v)
+    allowed = causal_allowed(tq, tk)[None]
+    torch.testing.assert_close(out.double(), naive_dense(q, k, v, allowed), atol=1e-5, rtol=1e-5)
+
+
+def test_prefill_is_causal():
+    # reference tests/test_attention.py:33-44
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(1, 2, 5, 8, generator=g) for _ in range(3))
+    before = torch_ref.prefill(q, k, v)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, -1] += 10
+    v2[:, :, -1] += 10
+    after = torch_ref.prefill(q, k2, v2)
+    torch.testing.assert_close(before[:, :, :-1], after[:, :, :-1])
+    assert not torch.allclose(before[:, :, -1], after[:, :, -1])
+
+
+def test_prefill_key_valid_own_slot_rule():
+    # left padding: query 0 has no real key and sees only its own position, the others skip key 0
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(1, n, 3, 8, generator=g) for n in (2, 1, 1))
+    key_valid = torch.tensor([[False, True, True]])
+    out = torch_ref.prefill(q, k, v, key_valid=key_valid)
+    allowed = torch.tensor([[[True, False, False], [False, True, False], [False, True, True]]])
+    torch.testing.assert_close(out.double(), naive_dense(q, k, v, allowed), atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(out[0, :, 0], v[0, 0, 0].expand(2, 8))
