@@ -88,7 +88,7 @@ int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_stride_head, c
  *   multi-token rows: one int2 item {seq, first_new_token} per tile of q_tile_tokens new tokens,
  *     last tile of each row first -> prefill_work[num_prefill_work].
  * The caller computes the three counts from the same host facts (sequence lengths and new-token
- * counts); the kernel writes at most that many items.  pages_per_split <= 64.
+ * counts); the kernel writes at most that many items.  pages_per_split <= 128.
  */
 int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, int32_t pages_per_split,
               int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work,

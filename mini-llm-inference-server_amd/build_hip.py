@@ -23,7 +23,9 @@ OUT_DIR = HERE / "minillm" / "_lib"
 LIB_NAME = "libminillm_hip.so"
 ARCH = os.environ.get("MLLM_OFFLOAD_ARCH", "gfx950")
 
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# no packed FP32; MFMA accumulators in VGPRs (the unified register file) rather than AGPRs, which
+# keeps the attention loops free of accumulator copies between the two register halves
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall",
                 "-Wno-unused-function"]
 

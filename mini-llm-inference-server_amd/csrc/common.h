@@ -59,22 +59,36 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
+// Packs two floats into one dword of 16-bit values (lo in bits 0-15), rounding to nearest even with
+// the hardware conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).  For the attention
+// kernels' P tiles and outputs; KV append keeps the bit-level conversion above, whose NaN encoding
+// is torch's.
 template <typename T>
-__device__ __forceinline__ uint16_t to_bits(float f);
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
 template <>
-__device__ __forceinline__ uint16_t to_bits<BF16>(float f) { return f32_to_bf16_bits(f); }
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 template <>
-__device__ __forceinline__ uint16_t to_bits<F16>(float f) { return f32_to_f16_bits(f); }
-
-// Packs two floats into one dword of 16-bit values (lo in bits 0-15).
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)to_bits<T>(lo) | ((uint32_t)to_bits<T>(hi) << 16);
+__device__ __forceinline__ uint16_t cvt1(float f) {
+  return (uint16_t)(pack2<T>(f, 0.f) & 0xffffu);
 }
 
 // ---------------------------------------------------------------- memory
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Streaming load (non-temporal hint: the data is read once and should not displace reused lines).
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }

@@ -30,7 +30,7 @@ struct DecodeArgs {
   const uint16_t* kc;
   const uint16_t* vc;
   int64_t num_blocks;
-  int bs, H, Hkv, G;
+  int bs, H, Hkv, G, HG;
   const int32_t* qo_indptr;
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
@@ -44,36 +44,98 @@ struct DecodeArgs {
   float2* part_ml;
 };
 
-template <typename T>
+template <bool NT>
+__device__ __forceinline__ u32x4 ldkv(const char* p) {
+  if constexpr (NT)
+    return ld16_nt(p);
+  else
+    return ld16(p);
+}
+
+// Loads 16-token tile t of this wave's page range: K rows in the A layout of S^T = K Q^T (lane (c, g):
+// row c, dims 32 kk + 8 g .. +7) and V rows 4 g .. 4 g + 3 at dims 8 c .. 8 c + 7.
+template <bool NT>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t tok_stride, int64_t blk_stride, int my_page, int t, int tpp, int c,
-                                          int g, u32x4 (&ka)[4], u32x4 (&va)[4]) {
+                                          int64_t tok_stride, int64_t blk_stride, int page_lo, int page_hi, int t,
+                                          int tpp, int c, int g, u32x4 (&ka)[4], u32x4 (&va)[4]) {
   const int page = t / tpp;
   const int sub = t - page * tpp;
-  int blk = __builtin_amdgcn_readlane(my_page, page);
+  int blk = __builtin_amdgcn_readlane(page < 64 ? page_lo : page_hi, page & 63);
   if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
   const int64_t off = (int64_t)blk * blk_stride + (int64_t)(sub * 16) * tok_stride;
   const char* kp = reinterpret_cast<const char*>(kbase + off + c * tok_stride);
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) ka[kk] = ld16(kp + (32 * kk + 8 * g) * 2);
+  for (int kk = 0; kk < 4; ++kk) ka[kk] = ldkv<NT>(kp + (32 * kk + 8 * g) * 2);
   const char* vp = reinterpret_cast<const char*>(vbase + off + (4 * g) * tok_stride + 8 * c);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) va[i] = ld16(vp + (int64_t)i * tok_stride * 2);
+  for (int i = 0; i < 4; ++i) va[i] = ldkv<NT>(vp + (int64_t)i * tok_stride * 2);
 }
 
+// One 16-token tile: scores, online-softmax update, PV accumulation.
 template <typename T>
-__global__ __launch_bounds__(64 * kWaves) void decode_kernel(const DecodeArgs a) {
+__device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4], const u32x4 (&qf)[4],
+                                             float scale_log2, int tpos0, int len, int g, float& m_run, float& l_run,
+                                             f32x4 (&o)[8]) {
+  f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) sc = Mfma<T>::m16x16x32(ka[kk], qf[kk], sc);
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
+  if (tpos0 + 16 > len) {  // the row's last, partly filled tile: mask the keys past its end, zero their V
+    const int tpos = tpos0 + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tpos + i >= len) {
+        s[i] = -INFINITY;
+        va[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = fast_exp2(m_run - m_new);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_new);
+  float ps = (p[0] + p[1]) + (p[2] + p[3]);
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  l_run = l_run * alpha + ps;
+  m_run = m_new;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) o[m] *= alpha;
+  const u32x2 pfrag = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int dw = m >> 1, hf = m & 1;
+    const u32x2 vfrag = u32x2{pick_halves(va[0][dw], hf, va[1][dw], hf), pick_halves(va[2][dw], hf, va[3][dw], hf)};
+    o[m] = Mfma<T>::m16x16x16(vfrag, pfrag, o[m]);
+  }
+}
+
+// PF: tiles loaded ahead of the one being consumed (a ring of PF + 1 register tiles).
+template <typename T, int PF, bool NT, int OCC>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_kernel(
+    const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
-  const int kvh = blockIdx.y * kWaves + (threadIdx.x >> 6);
+  // the KV-head group varies fastest, so the workgroups of one item (adjacent heads of the same
+  // pages) run side by side
+  const int hg = blockIdx.x % a.HG;
+  const int item = blockIdx.x / a.HG;
+  const int kvh = hg * kWaves + (threadIdx.x >> 6);
   if (kvh >= a.Hkv) return;  // wave-uniform
-  const int4 w = a.work[blockIdx.x];
-  const int seq = w.x, split = w.y, nsplit = w.z;
+  const int4 w = a.work[item];
+  const int seq = w.x, split = w.y, nsplit = w.z, slot = w.w;
   if (seq < 0) return;  // unfilled plan slot (the host pre-fills the plan with -1)
   const int pg0 = a.kv_indptr[seq];
-  const int pgn = a.kv_indptr[seq + 1];
+  const int npg = a.kv_indptr[seq + 1] - pg0;
   const int len = a.seq_lens[seq];
-  const int pb = pg0 + split * a.C;
-  const int pe = min(pgn, pb + a.C);
+  // balanced split: pages [split * P / ns, (split + 1) * P / ns)
+  const int pb = pg0 + (int)(((int64_t)split * npg) / nsplit);
+  const int pe = pg0 + (int)(((int64_t)(split + 1) * npg) / nsplit);
   const int tok0 = (pb - pg0) * a.bs;
   const int tok1 = min(len, (pe - pg0) * a.bs);
   const int ntiles = (tok1 - tok0 + 15) >> 4;
@@ -82,7 +144,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(const DecodeArgs a)
   const int g = lane >> 4;
   const int qtok = a.qo_indptr[seq];
 
-  const int my_page = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
+  // the split's page ids, one per lane (pages 0-63 and 64-127 of the split)
+  const int page_lo = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
+  const int page_hi = lane + 64 < (pe - pb) ? a.kv_indices[pb + 64 + lane] : 0;
 
   // B operand of S^T = K Q^T: lane (c, g) holds q head c of the group at dims 32 kk + 8 g .. +7.
   const bool qvalid = c < a.G;
@@ -107,56 +171,21 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(const DecodeArgs a)
 #pragma unroll
   for (int m = 0; m < 8; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 ka[4], va[4];
-  load_tile<T>(a, kbase, vbase, tok_stride, blk_stride, my_page, 0, tpp, c, g, ka, va);
-  for (int t = 0; t < ntiles; ++t) {
-    u32x4 kn[4], vn[4];
-    if (t + 1 < ntiles) load_tile<T>(a, kbase, vbase, tok_stride, blk_stride, my_page, t + 1, tpp, c, g, kn, vn);
-
-    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int R = PF + 1;
+  u32x4 kb[R][4], vb[R][4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) sc = Mfma<T>::m16x16x32(ka[kk], qf[kk], sc);
-
-    float s[4];
+  for (int r = 0; r < PF; ++r)
+    if (r < ntiles) load_tile<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, r, tpp, c, g, kb[r], vb[r]);
+  for (int t0 = 0; t0 < ntiles; t0 += R) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = sc[i] * a.scale_log2;
-    const int tpos = tok0 + t * 16 + 4 * g;  // context position of this lane's first row
-    if (tok0 + t * 16 + 16 > len) {           // the row's last, partly filled tile
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (tpos + i >= len) {
-          s[i] = -INFINITY;
-          va[i] = u32x4{0, 0, 0, 0};
-        }
+    for (int r = 0; r < R; ++r) {
+      const int t = t0 + r;
+      if (t < ntiles) {
+        if (t + PF < ntiles)
+          load_tile<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, t + PF, tpp, c, g,
+                        kb[(r + PF) % R], vb[(r + PF) % R]);
+        consume_tile<T>(kb[r], vb[r], qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
       }
-    }
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_new);
-    float ps = (p[0] + p[1]) + (p[2] + p[3]);
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) o[m] *= alpha;
-
-    const u32x2 pfrag = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int dw = m >> 1, hf = m & 1;
-      const u32x2 vfrag = u32x2{pick_halves(va[0][dw], hf, va[1][dw], hf), pick_halves(va[2][dw], hf, va[3][dw], hf)};
-      o[m] = Mfma<T>::m16x16x16(vfrag, pfrag, o[m]);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      ka[kk] = kn[kk];
-      va[kk] = vn[kk];
     }
   }
 
@@ -173,7 +202,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(const DecodeArgs a)
       st16(op + 16 * i, pk);
     }
   } else {
-    const int64_t row = (int64_t)blockIdx.x * a.H + head;
+    const int64_t row = (int64_t)slot * a.H + head;
     float* po = a.part_o + row * kHeadDim + 32 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -206,13 +235,20 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
     acc += wgt * part_o[row * kHeadDim + d];
   }
   const int qtok = qo_indptr[seq];
-  out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = to_bits<T>(acc / lsum);
+  out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = cvt1<T>(acc / lsum);
 }
+
+// Tuned on MI355X (decode_256 workload): one tile of lookahead with non-temporal K/V loads at 3
+// wavefronts per SIMD streams at 6.2 TB/s, the same as a two-tile lookahead at 2 per SIMD; forcing 4
+// per SIMD spills.
+constexpr int kPrefetch = 1;
+constexpr bool kNonTemporal = true;
+constexpr int kOccupancy = 3;
 
 template <typename T>
 int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
-  dim3 grid(n_work, (a.Hkv + kWaves - 1) / kWaves);
-  decode_kernel<T><<<grid, 64 * kWaves, 0, st>>>(a);
+  const unsigned grid = (unsigned)n_work * (unsigned)a.HG;
+  decode_kernel<T, kPrefetch, kNonTemporal, kOccupancy><<<grid, 64 * kWaves, 0, st>>>(a);
   return check_launch("mllm_paged_decode");
 }
 
@@ -242,8 +278,8 @@ extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_
                "mllm_paged_decode: num_heads must be a multiple of num_kv_heads");
   MLLM_REQUIRE(num_heads / num_kv_heads <= 16, MLLM_ERR_UNSUPPORTED,
                "mllm_paged_decode: at most 16 query heads per KV head");
-  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 64, MLLM_ERR_INVALID,
-               "mllm_paged_decode: pages_per_split must be in [1, 64]");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
+               "mllm_paged_decode: pages_per_split must be in [1, 128]");
   MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID, "mllm_paged_decode: negative count");
   if (num_decode_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && decode_work,
@@ -268,6 +304,7 @@ extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_
   a.H = num_heads;
   a.Hkv = num_kv_heads;
   a.G = num_heads / num_kv_heads;
+  a.HG = (num_kv_heads + kWaves - 1) / kWaves;
   a.qo_indptr = qo_indptr;
   a.kv_indptr = kv_indptr;
   a.kv_indices = kv_indices;

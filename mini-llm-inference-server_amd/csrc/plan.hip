@@ -1,15 +1,17 @@
 // Per-step work plan, built on the GPU once per step and reused by every layer (the role of
 // FlashInfer's plan(), reference src/minillm/attention/flashinfer_backend.py:44-64).
 //
-// One workgroup scans the S sequences: a decode row (one new token) becomes ceil(pages / C) split-KV
-// items of C pages; a row with several new tokens becomes ceil(new / q_tile) prefill tiles, the
-// tile with the longest causal context first.  Three exclusive scans give each row its item offsets.
+// One workgroup scans the S sequences: a decode row (one new token) of P pages becomes ns = ceil(P / C)
+// split-KV items of P / ns pages each (balanced), listed largest first (a counting sort on the size);
+// a row with several new tokens becomes ceil(new / q_tile) prefill tiles, the tile with the longest
+// causal context first.  Exclusive scans give each row its item offsets.
 #include "common.h"
 
 namespace mllm {
 namespace {
 
 constexpr int kPlanThreads = 1024;
+constexpr int kMaxSplitPages = 128;
 
 __device__ __forceinline__ int wg_exclusive_scan(int v, int* sums, int* total) {
   const int lane = threadIdx.x & 63;
@@ -46,13 +48,40 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
                                                             int4* __restrict__ merge_work, int32_t cap_merge,
                                                             int2* __restrict__ prefill_work, int32_t cap_prefill) {
   __shared__ int sums[kPlanThreads / 64];
+  __shared__ int hist[kMaxSplitPages + 1];  // decode items per size in pages
+  __shared__ int offs[kMaxSplitPages + 1];  // next free position of each size class
+  for (int i = threadIdx.x; i <= kMaxSplitPages; i += blockDim.x) hist[i] = 0;
+  __syncthreads();
+  // pass 1: sizes of the decode items.  A row of P pages gets ns = ceil(P / C) splits of P / ns pages
+  // (the first P % ns of them one page more), so every split of a long row holds C/2 .. C pages.
+  for (int base = 0; base < num_seqs; base += kPlanThreads) {
+    const int s = base + threadIdx.x;
+    if (s < num_seqs && qo_indptr[s + 1] - qo_indptr[s] == 1) {
+      const int pages = kv_indptr[s + 1] - kv_indptr[s];
+      const int ns = (pages + pages_per_split - 1) / pages_per_split;
+      const int q = pages / ns, rem = pages - q * ns;
+      atomicAdd(&hist[q], ns - rem);
+      if (rem) atomicAdd(&hist[q + 1], rem);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // largest items first: the short ones fill the tail of the launch
+    int run = 0;
+    for (int sz = kMaxSplitPages; sz >= 1; --sz) {
+      offs[sz] = run;
+      run += hist[sz];
+    }
+  }
+  __syncthreads();
+  // pass 2: emit.  A decode item carries its row's canonical partial slot (row-major order), which is
+  // where the merge looks for it whatever its position in the launch.
   int base_d = 0, base_m = 0, base_p = 0;
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
     const int s = base + threadIdx.x;
-    int nd = 0, nm = 0, np = 0, nn = 0;
+    int nd = 0, nm = 0, np = 0, pages = 0;
     if (s < num_seqs) {
-      nn = qo_indptr[s + 1] - qo_indptr[s];
-      const int pages = kv_indptr[s + 1] - kv_indptr[s];
+      const int nn = qo_indptr[s + 1] - qo_indptr[s];
+      pages = kv_indptr[s + 1] - kv_indptr[s];
       if (nn == 1) {
         nd = (pages + pages_per_split - 1) / pages_per_split;
         nm = nd > 1 ? 1 : 0;
@@ -64,8 +93,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
     const int od = base_d + wg_exclusive_scan(nd, sums, &td);
     const int om = base_m + wg_exclusive_scan(nm, sums, &tm);
     const int op = base_p + wg_exclusive_scan(np, sums, &tp);
-    for (int j = 0; j < nd; ++j)
-      if (od + j < cap_decode) decode_work[od + j] = make_int4(s, j, nd, od);
+    for (int j = 0; j < nd; ++j) {
+      const int sz = (int)(((int64_t)(j + 1) * pages) / nd - ((int64_t)j * pages) / nd);
+      const int pos = atomicAdd(&offs[sz], 1);
+      if (pos < cap_decode) decode_work[pos] = make_int4(s, j, nd, od + j);
+    }
     if (nm && om < cap_merge) merge_work[om] = make_int4(s, od, nd, 0);
     for (int j = 0; j < np; ++j)
       if (op + j < cap_prefill) prefill_work[op + j] = make_int2(s, (np - 1 - j) * q_tile);
@@ -84,8 +116,8 @@ extern "C" int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int
                          int32_t num_prefill_work, void* stream) {
   using namespace mllm;
   MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, "mllm_plan: num_seqs < 0");
-  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 64, MLLM_ERR_INVALID,
-               "mllm_plan: pages_per_split must be in [1, 64]");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
+               "mllm_plan: pages_per_split must be in [1, 128]");
   MLLM_REQUIRE(q_tile_tokens >= 1, MLLM_ERR_INVALID, "mllm_plan: q_tile_tokens must be positive");
   MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0 && num_prefill_work >= 0, MLLM_ERR_INVALID,
                "mllm_plan: negative capacity");

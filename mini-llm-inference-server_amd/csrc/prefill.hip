@@ -16,7 +16,7 @@
 // S^T and P^T share a lane layout (lane l: row l % 32), so the online softmax (fp32, exp2 domain)
 // reduces each row's max and sum inside the lane plus one exchange with lane l ^ 32, and P^T feeds
 // the PV product without leaving its lanes.  Tiles entirely above a wavefront's causal diagonal are
-// skipped; keys past the tile's causal limit are never loaded (zeros in LDS).  The grid is 1-D with
+// skipped; keys past the tile's causal limit are stored to LDS as zeros.  The grid is 1-D with
 // the KV head fastest, so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs)
 // serves one KV head and keeps that head's shared-prefix pages in its own L2.
 #include <math.h>
@@ -40,7 +40,7 @@ struct PrefillArgs {
   const uint16_t* kc;
   const uint16_t* vc;
   int64_t num_blocks;
-  int bs, H, Hkv, G;
+  int bs, bs_shift, H, Hkv, G;
   const int32_t* qo_indptr;
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
@@ -57,22 +57,20 @@ __device__ __forceinline__ int vt_pos(int key) {
   return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
 }
 
+// Page ids of this thread's keys in one K/V tile.  Loaded without branches (a key past the tile's causal
+// limit reads the id of the limit's page instead), so the compiler never has to wait on them before
+// the tile is needed; validity is applied when the tile is stored to LDS.
 struct TileIds {
-  int k[4];  // block id of each of this thread's 4 K keys (-1: past the causal limit)
-  int v;     // block id of this thread's 4 V keys
+  int k[4];  // block of each of this thread's 4 K keys
+  int v;     // block of this thread's 4 V keys
 };
-
-__device__ __forceinline__ int block_of(const PrefillArgs& a, int pg0, int key, int kv_end) {
-  if (key >= kv_end) return -1;
-  int b = a.kv_indices[pg0 + key / a.bs];
-  return ((unsigned)b < (unsigned)a.num_blocks) ? b : -1;
-}
 
 __device__ __forceinline__ TileIds load_ids(const PrefillArgs& a, int pg0, int kv0, int kv_end, int tid) {
   TileIds ids;
+  const int last = kv_end - 1;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ids.k[j] = block_of(a, pg0, kv0 + tid / 16 + 16 * j, kv_end);
-  ids.v = block_of(a, pg0, kv0 + 4 * (tid & 15), kv_end);
+  for (int j = 0; j < 4; ++j) ids.k[j] = a.kv_indices[pg0 + (min(kv0 + tid / 16 + 16 * j, last) >> a.bs_shift)];
+  ids.v = a.kv_indices[pg0 + (min(kv0 + 4 * (tid & 15), last) >> a.bs_shift)];
   return ids;
 }
 
@@ -81,46 +79,49 @@ struct TileRegs {
   u32x4 v[4];
 };
 
-__device__ __forceinline__ TileRegs load_data(const PrefillArgs& a, const TileIds& ids, int kv0, int kv_end, int kvh,
-                                              int tid) {
+__device__ __forceinline__ int64_t pool_row(const PrefillArgs& a, int blk, int key) {
+  blk = ((unsigned)blk < (unsigned)a.num_blocks) ? blk : 0;  // never taken with valid metadata
+  return ((int64_t)blk << a.bs_shift) + (key & (a.bs - 1));
+}
+
+// Issues the tile's global loads (unconditionally: rows past the causal limit are read from a valid
+// slot of the same pool and zeroed in store_tile).
+__device__ __forceinline__ TileRegs load_data(const PrefillArgs& a, const TileIds& ids, int kv0, int kvh, int tid) {
   TileRegs r;
   const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int key = kv0 + tid / 16 + 16 * j;
-    if (ids.k[j] >= 0) {
-      const int64_t row = (int64_t)ids.k[j] * a.bs + key % a.bs;
-      r.k[j] = ld16(a.kc + row * tok_stride + kvh * kHeadDim + 8 * (tid & 15));
-    } else {
-      r.k[j] = u32x4{0, 0, 0, 0};
-    }
+    const int64_t row = pool_row(a, ids.k[j], kv0 + tid / 16 + 16 * j);
+    r.k[j] = ld16(a.kc + row * tok_stride + kvh * kHeadDim + 8 * (tid & 15));
   }
   const int key0 = kv0 + 4 * (tid & 15);
-  const int dc = tid >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (ids.v >= 0 && key0 + i < kv_end) {
-      const int64_t row = (int64_t)ids.v * a.bs + (key0 + i) % a.bs;
-      r.v[i] = ld16(a.vc + row * tok_stride + kvh * kHeadDim + 8 * dc);
-    } else {
-      r.v[i] = u32x4{0, 0, 0, 0};
-    }
+    const int64_t row = pool_row(a, ids.v, key0 + i);
+    r.v[i] = ld16(a.vc + row * tok_stride + kvh * kHeadDim + 8 * (tid >> 4));
   }
   return r;
 }
 
-__device__ __forceinline__ void store_tile(uint16_t* buf, const TileRegs& r, int tid) {
+__device__ __forceinline__ void store_tile(uint16_t* buf, const TileRegs& r, int kv0, int kv_end, int tid) {
   uint16_t* ks = buf;
   uint16_t* vt = buf + kKsElems;
+  const u32x4 zero = u32x4{0, 0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) st16(ks + (tid / 16 + 16 * j) * kKs + 8 * (tid & 15), r.k[j]);
+  for (int j = 0; j < 4; ++j) {
+    const bool ok = kv0 + tid / 16 + 16 * j < kv_end;
+    st16(ks + (tid / 16 + 16 * j) * kKs + 8 * (tid & 15), ok ? r.k[j] : zero);
+  }
   // V: this thread holds keys 4kg .. 4kg+3 at dims 8dc .. 8dc+7; write, per dim, the 4 keys as 8 bytes.
   const int kg = tid & 15, dc = tid >> 4;
   const int pos = vt_pos(4 * kg);
+  u32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = kv0 + 4 * kg + i < kv_end ? r.v[i] : zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int dw = e >> 1, hf = e & 1;
-    u32x2 pk = u32x2{pick_halves(r.v[0][dw], hf, r.v[1][dw], hf), pick_halves(r.v[2][dw], hf, r.v[3][dw], hf)};
+    u32x2 pk = u32x2{pick_halves(v[0][dw], hf, v[1][dw], hf), pick_halves(v[2][dw], hf, v[3][dw], hf)};
     st8(vt + (8 * dc + e) * kVt + pos, pk);
   }
 }
@@ -153,6 +154,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int qp = row_valid ? cached + tok : len - 1;  // context position of the row's token
   const int wave_tok_hi = min(t0 + wave * tpw + tpw, nn) - 1;
   const int wave_qp_hi = wave_tok_hi >= t0 + wave * tpw ? cached + wave_tok_hi : -1;  // -1: no valid row
+  const int wave_qp_lo = cached + t0 + wave * tpw;  // position of the wavefront's first row
 
   // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7.
   u32x4 qf[8];
@@ -174,15 +176,15 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
 
   TileIds ids_next = load_ids(a, pg0, 0, kv_end, tid);
-  TileRegs regs = load_data(a, ids_next, 0, kv_end, kvh, tid);
+  TileRegs regs = load_data(a, ids_next, 0, kvh, tid);
   if (ntiles > 1) ids_next = load_ids(a, pg0, kBN, kv_end, tid);
-  store_tile(lds, regs, tid);
+  store_tile(lds, regs, 0, kv_end, tid);
   __syncthreads();
 
   for (int it = 0; it < ntiles; ++it) {
     const int kv0 = it * kBN;
     if (it + 1 < ntiles) {
-      regs = load_data(a, ids_next, kv0 + kBN, kv_end, kvh, tid);
+      regs = load_data(a, ids_next, kv0 + kBN, kvh, tid);
       if (it + 2 < ntiles) ids_next = load_ids(a, pg0, kv0 + 2 * kBN, kv_end, tid);
     }
     const uint16_t* ks = lds + (it & 1) * kBufElems;
@@ -198,38 +200,46 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) sacc[b] = Mfma<T>::m32x32x16(ld16(krow + 16 * kk), qf[kk], sacc[b]);
       }
-      // sacc[b][r]: key 32 b + 8 (r / 4) + 4 h + r % 4 of row n
-      const bool need_mask = kv0 + kBN - 1 > qp || kv0 + kBN > kv_end;
+      // sacc[b][r]: raw score of key kv0 + 32 b + 8 (r / 4) + 4 h + r % 4 for row n.  Only tiles that
+      // reach past the wavefront's first row need the causal mask (a wave-uniform test).
+      if (kv0 + kBN - 1 > wave_qp_lo) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+            sacc[b][r] = key > qp ? -INFINITY : sacc[b][r];
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float s = sacc[b][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (key > qp) s = -INFINITY;
-          }
-          sacc[b][r] = s;
-          mx = fmaxf(mx, s);
-        }
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[b][r], sacc[b][r + 1]));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
+      // Lazy rescale: the running max only moves (and O, l are rescaled) when some row's max grew by
+      // more than 2^8 in the exp2 domain; otherwise p = 2^((s - m) c) stays below 256, which fp32
+      // accumulation and the bf16 P operand hold exactly as well as values below 1.
+      if (__any((mx - m_run) * a.scale_log2 > 8.f)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2((m_run - m_new) * a.scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+        m_run = m_new;
+      }
+      const float mc = m_run * a.scale_log2;
       float ps = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[b][r] - m_new);
+          const float p = fast_exp2(__builtin_fmaf(sacc[b][r], a.scale_log2, -mc));
           sacc[b][r] = p;
           ps += p;
         }
       ps += __shfl_xor(ps, 32, 64);
-      l_run = l_run * alpha + ps;
-      m_run = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+      l_run += ps;
 
 #pragma unroll
       for (int b = 0; b < 2; ++b)
@@ -244,7 +254,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         }
     }
 
-    if (it + 1 < ntiles) store_tile(lds + ((it + 1) & 1) * kBufElems, regs, tid);
+    if (it + 1 < ntiles) store_tile(lds + ((it + 1) & 1) * kBufElems, regs, kv0 + kBN, kv_end, tid);
     __syncthreads();
   }
 
@@ -278,8 +288,8 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
                "mllm_paged_prefill: dtype must be bfloat16 or float16");
   MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: head_dim must be 128");
-  MLLM_REQUIRE(block_size > 0 && block_size % 16 == 0, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_prefill: block_size must be a multiple of 16");
+  MLLM_REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0, MLLM_ERR_UNSUPPORTED,
+               "mllm_paged_prefill: block_size must be a power of two >= 16");
   MLLM_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, MLLM_ERR_INVALID,
                "mllm_paged_prefill: num_heads must be a multiple of num_kv_heads");
   const int G = num_heads / num_kv_heads;
@@ -303,6 +313,7 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   a.vc = static_cast<const uint16_t*>(v_cache);
   a.num_blocks = num_blocks;
   a.bs = block_size;
+  a.bs_shift = __builtin_ctz((unsigned)block_size);
   a.H = num_heads;
   a.Hkv = num_kv_heads;
   a.G = G;

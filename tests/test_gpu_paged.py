@@ -55,13 +55,15 @@ def test_metadata_random_steps(hip, bs, seed):
     from minillm.attention.metadata import AttentionMetadata, SeqStep
 
     rng = random.Random(seed)
-    perm = list(range(200000))
-    rng.shuffle(perm)
-    seqs, o = [], 0
+    steps = []
     for _ in range(rng.randrange(1, 1500)):
         cached = rng.choice([0, rng.randrange(0, 3000)])
         new = rng.choice([1, 1, 1, rng.randrange(1, 300)])
-        need = -(-(cached + new) // bs) + rng.randrange(0, 3)
+        steps.append((cached, new, -(-(cached + new) // bs) + rng.randrange(0, 3)))
+    total = sum(need for _, _, need in steps)
+    perm = torch.randperm(total, generator=torch.Generator().manual_seed(seed)).tolist()
+    seqs, o = [], 0
+    for cached, new, need in steps:
         seqs.append((cached, new, perm[o:o + need]))
         o += need
     meta = AttentionMetadata.build([SeqStep(*s) for s in seqs], bs, DEV)
@@ -227,7 +229,9 @@ def test_plan_is_reused_per_metadata(hip):
 
 
 def test_plan_contents(hip):
-    # the GPU plan against the split rule it implements, on rows of many lengths
+    # the GPU plan against the split rule it implements, on rows of many lengths: a decode row of P
+    # pages gets ns = ceil(P / C) balanced splits with canonical partial slots; the launch order is
+    # largest split first
     from minillm.attention.hip_backend import HipBackend
     from minillm.attention.metadata import AttentionMetadata, SeqStep
 
@@ -250,13 +254,21 @@ def test_plan_contents(hip):
         if n == 1:
             ns = -(-pages // c)
             first = len(exp_dec)
-            exp_dec += [[s, j, ns, first] for j in range(ns)]
+            exp_dec += [[s, j, ns, first + j] for j in range(ns)]
             if ns > 1:
                 exp_merge.append([s, first, ns, 0])
         else:
             nt = -(-n // p.q_tile)
             exp_pf += [[s, (nt - 1 - j) * p.q_tile] for j in range(nt)]
-    assert dec == exp_dec
+    assert sorted(dec) == sorted(exp_dec)
+
+    def size(item):
+        s, j, ns, _ = item
+        pages = -(-sum(steps[s]) // 16)
+        return (j + 1) * pages // ns - j * pages // ns
+
+    sizes = [size(it) for it in dec]
+    assert sizes == sorted(sizes, reverse=True) and max(sizes) <= c
     assert p.merge_work.view(-1, 4).cpu().tolist() == exp_merge
     assert p.prefill_work.view(-1, 2).cpu().tolist() == exp_pf
 

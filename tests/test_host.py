@@ -96,9 +96,9 @@ def test_split_size_heuristic(monkeypatch):
 
     monkeypatch.delenv("MLLM_PAGES_PER_SPLIT", raising=False)
     assert hip_backend.pages_per_split(10, 8) == 8
-    assert hip_backend.pages_per_split(10 ** 7, 8) == 64
+    assert hip_backend.pages_per_split(10 ** 7, 8) == 128
     c = hip_backend.pages_per_split(34000, 8)
-    assert 8 <= c <= 64
+    assert 80 <= c <= 100
     monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", "5")
     assert hip_backend.pages_per_split(34000, 8) == 5
 
