@@ -5,8 +5,7 @@
 // One workgroup (4 wavefronts) per (q tile, KV head).  A q tile is 128 / G new tokens of one row,
 // times the G query heads that share the KV head: 128 MFMA rows, 32 per wavefront (rows are
 // token-major: row = token * G + head).  K/V are streamed in tiles of 64 keys gathered through
-// kv_indices into LDS (double-buffered; the next tile's global loads are in flight while the current
-// tile is consumed):
+// kv_indices into LDS:
 //   K  as Ks[key][dim]  (row stride 136 elements)
 //   V  as Vt[dim][key'] (row stride  72 elements), key' a permutation inside each 16-key group
 //      (bits 2 and 3 of the key swapped) so that the PV operand of every lane is one 16-byte read.
@@ -15,10 +14,17 @@
 //   O^T[128 x 32 rows]    += V^T . P^T   4 x 4 v_mfma_f32_32x32x16
 // S^T and P^T share a lane layout (lane l: row l % 32), so the online softmax (fp32, exp2 domain)
 // reduces each row's max and sum inside the lane plus one exchange with lane l ^ 32, and P^T feeds
-// the PV product without leaving its lanes.  Tiles entirely above a wavefront's causal diagonal are
-// skipped; keys past the tile's causal limit are stored to LDS as zeros.  The grid is 1-D with
-// the KV head fastest, so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs)
-// serves one KV head and keeps that head's shared-prefix pages in its own L2.
+// the PV product without leaving its lanes.
+//
+// Software pipeline (one barrier per tile): iteration i issues the score MFMAs of tile i + 1 first,
+// then runs tile i's softmax on the vector ALUs while those MFMAs execute, then tile i's PV MFMAs.
+// K is therefore staged in LDS two tiles ahead and V one tile ahead (two buffers each: K(i+2) is
+// stored over K(i), V(i+1) over V(i-1)), and the global loads for K(i+3) / V(i+2) are in flight
+// during the whole iteration.  Tiles entirely above a wavefront's causal diagonal are skipped; keys
+// past the tile's causal limit are stored to LDS as zeros.  The running max is rescaled lazily (see
+// the softmax below).  The grid is 1-D with the KV head fastest, so with 8 KV heads each XCD
+// (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and keeps that head's
+// shared-prefix pages in its own L2.
 #include <math.h>
 
 #include "common.h"
@@ -27,12 +33,11 @@ namespace mllm {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kBN = 64;          // keys per K/V tile
-constexpr int kKs = 136;         // Ks row stride (elements)
-constexpr int kVt = 72;          // Vt row stride (elements)
+constexpr int kBN = 64;   // keys per K/V tile
+constexpr int kKs = 136;  // Ks row stride (elements)
+constexpr int kVt = 72;   // Vt row stride (elements)
 constexpr int kKsElems = kBN * kKs;
 constexpr int kVtElems = kHeadDim * kVt;
-constexpr int kBufElems = kKsElems + kVtElems;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -40,6 +45,8 @@ struct PrefillArgs {
   const uint16_t* kc;
   const uint16_t* vc;
   int64_t num_blocks;
+  unsigned page_bytes;  // bytes of one block of one pool: bs * Hkv * Dh * 2 (< 2^32)
+  int row_bytes;        // bytes of one token row: Hkv * Dh * 2 (< 2^24)
   int bs, bs_shift, H, Hkv, G;
   const int32_t* qo_indptr;
   const int32_t* kv_indptr;
@@ -53,82 +60,116 @@ struct PrefillArgs {
 };
 
 // Key position -> position inside the permuted Vt row: within each 16-key group swap bits 2 and 3.
-__device__ __forceinline__ int vt_pos(int key) {
-  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
+__device__ __forceinline__ int vt_pos(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 
-// Page ids of this thread's keys in one K/V tile.  Loaded without branches (a key past the tile's causal
-// limit reads the id of the limit's page instead), so the compiler never has to wait on them before
-// the tile is needed; validity is applied when the tile is stored to LDS.
-struct TileIds {
-  int k[4];  // block of each of this thread's 4 K keys
-  int v;     // block of this thread's 4 V keys
+// Page ids are loaded without branches (a key past the causal limit reads the id of the limit's
+// page), so the compiler never waits on them early; validity is applied when a tile is stored.
+// Thread tid handles K keys tid / 16 + 16 j (j < 4), dims 8 (tid % 16) .. +7, and V keys
+// 4 (tid % 16) .. +3, dims 8 (tid / 16) .. +7.
+struct KIds {
+  int b[4];
 };
 
-__device__ __forceinline__ TileIds load_ids(const PrefillArgs& a, int pg0, int kv0, int kv_end, int tid) {
-  TileIds ids;
-  const int last = kv_end - 1;
+__device__ __forceinline__ KIds k_ids(const PrefillArgs& a, const int32_t* pages, int kv0, int last, int tid) {
+  KIds ids;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ids.k[j] = a.kv_indices[pg0 + (min(kv0 + tid / 16 + 16 * j, last) >> a.bs_shift)];
-  ids.v = a.kv_indices[pg0 + (min(kv0 + 4 * (tid & 15), last) >> a.bs_shift)];
+  for (int j = 0; j < 4; ++j) ids.b[j] = pages[(unsigned)min(kv0 + tid / 16 + 16 * j, last) >> a.bs_shift];
   return ids;
 }
 
-struct TileRegs {
-  u32x4 k[4];
-  u32x4 v[4];
-};
-
-__device__ __forceinline__ int64_t pool_row(const PrefillArgs& a, int blk, int key) {
-  blk = ((unsigned)blk < (unsigned)a.num_blocks) ? blk : 0;  // never taken with valid metadata
-  return ((int64_t)blk << a.bs_shift) + (key & (a.bs - 1));
+__device__ __forceinline__ int v_id(const PrefillArgs& a, const int32_t* pages, int kv0, int last, int tid) {
+  return pages[(unsigned)min(kv0 + 4 * (tid & 15), last) >> a.bs_shift];
 }
 
-// Issues the tile's global loads (unconditionally: rows past the causal limit are read from a valid
-// slot of the same pool and zeroed in store_tile).
-__device__ __forceinline__ TileRegs load_data(const PrefillArgs& a, const TileIds& ids, int kv0, int kvh, int tid) {
-  TileRegs r;
-  const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;
+// pool + block * page_bytes + slot * row_bytes + col_bytes (slot < block_size and row_bytes < 2^24, so
+// the in-page product is a 24-bit multiply).
+__device__ __forceinline__ const char* row_ptr(const char* pool, const PrefillArgs& a, int blk, int slot,
+                                               int col_bytes) {
+  const unsigned b = ((unsigned)blk < (unsigned)a.num_blocks) ? (unsigned)blk : 0u;  // else-branch never taken
+  const unsigned in_page = __umul24((unsigned)slot, (unsigned)a.row_bytes) + (unsigned)col_bytes;
+  return pool + ((uint64_t)b * a.page_bytes + in_page);
+}
+
+struct Regs4 {
+  u32x4 x[4];
+};
+
+// Global loads of one tile (issued unconditionally; rows past the causal limit come from a valid slot
+// and are zeroed when stored).
+__device__ __forceinline__ Regs4 load_k(const PrefillArgs& a, const KIds& ids, int kv0, int kvh, int tid) {
+  Regs4 r;
+  const char* kc = reinterpret_cast<const char*>(a.kc);
+  const int col = kvh * kHeadDim * 2 + 16 * (tid & 15);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t row = pool_row(a, ids.k[j], kv0 + tid / 16 + 16 * j);
-    r.k[j] = ld16(a.kc + row * tok_stride + kvh * kHeadDim + 8 * (tid & 15));
-  }
-  const int key0 = kv0 + 4 * (tid & 15);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = pool_row(a, ids.v, key0 + i);
-    r.v[i] = ld16(a.vc + row * tok_stride + kvh * kHeadDim + 8 * (tid >> 4));
-  }
+  for (int j = 0; j < 4; ++j) r.x[j] = ld16(row_ptr(kc, a, ids.b[j], (kv0 + tid / 16 + 16 * j) & (a.bs - 1), col));
   return r;
 }
 
-__device__ __forceinline__ void store_tile(uint16_t* buf, const TileRegs& r, int kv0, int kv_end, int tid) {
-  uint16_t* ks = buf;
-  uint16_t* vt = buf + kKsElems;
-  const u32x4 zero = u32x4{0, 0, 0, 0};
+__device__ __forceinline__ Regs4 load_v(const PrefillArgs& a, int id, int kv0, int kvh, int tid) {
+  Regs4 r;
+  const char* vp = row_ptr(reinterpret_cast<const char*>(a.vc), a, id, (kv0 + 4 * (tid & 15)) & (a.bs - 1),
+                           kvh * kHeadDim * 2 + 16 * (tid >> 4));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool ok = kv0 + tid / 16 + 16 * j < kv_end;
-    st16(ks + (tid / 16 + 16 * j) * kKs + 8 * (tid & 15), ok ? r.k[j] : zero);
+  for (int i = 0; i < 4; ++i) r.x[i] = ld16(vp + i * a.row_bytes);
+  return r;
+}
+
+// LDS stores of one tile; keys at or past kv_end become zeros (only a row's last tile has any).
+__device__ __forceinline__ void store_k(uint16_t* ks, Regs4 r, int kv0, int kv_end, int tid) {
+  if (kv0 + kBN > kv_end) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.x[j] = kv0 + tid / 16 + 16 * j < kv_end ? r.x[j] : u32x4{0, 0, 0, 0};
   }
-  // V: this thread holds keys 4kg .. 4kg+3 at dims 8dc .. 8dc+7; write, per dim, the 4 keys as 8 bytes.
-  const int kg = tid & 15, dc = tid >> 4;
-  const int pos = vt_pos(4 * kg);
-  u32x4 v[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = kv0 + 4 * kg + i < kv_end ? r.v[i] : zero;
+  for (int j = 0; j < 4; ++j) st16(ks + (tid / 16 + 16 * j) * kKs + 8 * (tid & 15), r.x[j]);
+}
+
+__device__ __forceinline__ void store_v(uint16_t* vt, Regs4 r, int kv0, int kv_end, int tid) {
+  const int kg = tid & 15, dc = tid >> 4;
+  if (kv0 + kBN > kv_end) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.x[i] = kv0 + 4 * kg + i < kv_end ? r.x[i] : u32x4{0, 0, 0, 0};
+  }
+  // this thread holds keys 4kg .. 4kg+3 at dims 8dc .. 8dc+7; write, per dim, the 4 keys as 8 bytes
+  const int pos = vt_pos(4 * kg);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int dw = e >> 1, hf = e & 1;
-    u32x2 pk = u32x2{pick_halves(v[0][dw], hf, v[1][dw], hf), pick_halves(v[2][dw], hf, v[3][dw], hf)};
+    const u32x2 pk =
+        u32x2{pick_halves(r.x[0][dw], hf, r.x[1][dw], hf), pick_halves(r.x[2][dw], hf, r.x[3][dw], hf)};
     st8(vt + (8 * dc + e) * kVt + pos, pk);
   }
 }
 
+struct STile {
+  f32x16 s[2];  // s[b][r]: key 32 b + 8 (r / 4) + 4 h + r % 4 of the tile, row n
+};
+
+// The two 32-key halves are independent accumulation chains; alternating them keeps two MFMAs in
+// flight instead of waiting on each accumulator in turn.
+template <typename T>
+__device__ __forceinline__ STile scores(const uint16_t* ks, const u32x4 (&qf)[8], int n, int h) {
+  STile t;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t.s[b][r] = 0.f;
+  const uint16_t* krow = ks + n * kKs + 8 * h;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const u32x4 k0 = ld16(krow + 16 * kk);
+    const u32x4 k1 = ld16(krow + 32 * kKs + 16 * kk);
+    t.s[0] = Mfma<T>::m32x32x16(k0, qf[kk], t.s[0]);
+    t.s[1] = Mfma<T>::m32x32x16(k1, qf[kk], t.s[1]);
+  }
+  return t;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kKsElems + 2 * kVtElems];
+  uint16_t* const kbuf0 = lds;
+  uint16_t* const vbuf0 = lds + 2 * kKsElems;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -140,11 +181,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int nn = a.qo_indptr[seq + 1] - qs;
   const int len = a.seq_lens[seq];
   const int cached = len - nn;
-  const int pg0 = a.kv_indptr[seq];
+  const int32_t* pages = a.kv_indices + a.kv_indptr[seq];
   const int tpw = 32 / a.G;  // tokens per wavefront
   const int qt_valid = min(a.QT, nn - t0);
   // keys any row of this workgroup may see
   const int kv_end = min(len, cached + t0 + qt_valid);
+  const int last = kv_end - 1;
   const int ntiles = (kv_end + kBN - 1) / kBN;
 
   // this lane's row
@@ -160,10 +202,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   u32x4 qf[8];
   {
     const int head = kvh * a.G + (n % a.G);
-    const uint16_t* qp_row = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
+    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      u32x4 v = ld16(qp_row + 16 * kk + 8 * h);
+      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
       qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
     }
   }
@@ -175,47 +217,47 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  TileIds ids_next = load_ids(a, pg0, 0, kv_end, tid);
-  TileRegs regs = load_data(a, ids_next, 0, kvh, tid);
-  if (ntiles > 1) ids_next = load_ids(a, pg0, kBN, kv_end, tid);
-  store_tile(lds, regs, 0, kv_end, tid);
+  // prologue: K(0), K(1), V(0) into LDS; K(2), V(1) in registers; ids of K(3), V(2)
+  {
+    const Regs4 k0 = load_k(a, k_ids(a, pages, 0, last, tid), 0, kvh, tid);
+    const Regs4 v0 = load_v(a, v_id(a, pages, 0, last, tid), 0, kvh, tid);
+    store_k(kbuf0, k0, 0, kv_end, tid);
+    store_v(vbuf0, v0, 0, kv_end, tid);
+    if (ntiles > 1)
+      store_k(kbuf0 + kKsElems, load_k(a, k_ids(a, pages, kBN, last, tid), kBN, kvh, tid), kBN, kv_end, tid);
+  }
+  Regs4 kr, vr;
+  if (ntiles > 2) kr = load_k(a, k_ids(a, pages, 2 * kBN, last, tid), 2 * kBN, kvh, tid);
+  if (ntiles > 1) vr = load_v(a, v_id(a, pages, kBN, last, tid), kBN, kvh, tid);
+  KIds kid_next = k_ids(a, pages, 3 * kBN, last, tid);
+  int vid_next = v_id(a, pages, 2 * kBN, last, tid);
   __syncthreads();
+  STile cur;
+  if (0 <= wave_qp_hi) cur = scores<T>(kbuf0, qf, n, h);
+  __syncthreads();  // every wavefront has read K(0) before iteration 0 overwrites it with K(2)
 
   for (int it = 0; it < ntiles; ++it) {
     const int kv0 = it * kBN;
-    if (it + 1 < ntiles) {
-      regs = load_data(a, ids_next, kv0 + kBN, kvh, tid);
-      if (it + 2 < ntiles) ids_next = load_ids(a, pg0, kv0 + 2 * kBN, kv_end, tid);
-    }
-    const uint16_t* ks = lds + (it & 1) * kBufElems;
-    const uint16_t* vt = ks + kKsElems;
+    // 1. score MFMAs of the next tile, issued ahead of this tile's softmax
+    STile nxt;
+    if (it + 1 < ntiles && kv0 + kBN <= wave_qp_hi) nxt = scores<T>(kbuf0 + ((it + 1) & 1) * kKsElems, qf, n, h);
 
+    // 2. softmax and PV of this tile
     if (kv0 <= wave_qp_hi) {  // some key of this tile is visible to some row of this wavefront
-      f32x16 sacc[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
-        const uint16_t* krow = ks + (32 * b + n) * kKs + 8 * h;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) sacc[b] = Mfma<T>::m32x32x16(ld16(krow + 16 * kk), qf[kk], sacc[b]);
-      }
-      // sacc[b][r]: raw score of key kv0 + 32 b + 8 (r / 4) + 4 h + r % 4 for row n.  Only tiles that
-      // reach past the wavefront's first row need the causal mask (a wave-uniform test).
-      if (kv0 + kBN - 1 > wave_qp_lo) {
+      if (kv0 + kBN - 1 > wave_qp_lo) {  // the tile reaches past the wavefront's first row: causal mask
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-            sacc[b][r] = key > qp ? -INFINITY : sacc[b][r];
+            cur.s[b][r] = key > qp ? -INFINITY : cur.s[b][r];
           }
       }
       float mx = -INFINITY;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[b][r], sacc[b][r + 1]));
+        for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, cur.s[b][r]), cur.s[b][r + 1]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       // Lazy rescale: the running max only moves (and O, l are rescaled) when some row's max grew by
       // more than 2^8 in the exp2 domain; otherwise p = 2^((s - m) c) stays below 256, which fp32
@@ -234,28 +276,38 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(__builtin_fmaf(sacc[b][r], a.scale_log2, -mc));
-          sacc[b][r] = p;
+          const float p = fast_exp2(__builtin_fmaf(cur.s[b][r], a.scale_log2, -mc));
+          cur.s[b][r] = p;
           ps += p;
         }
       ps += __shfl_xor(ps, 32, 64);
       l_run += ps;
 
+      const uint16_t* vt = vbuf0 + (it & 1) * kVtElems;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int r0 = 8 * u;
-          const u32x4 pfrag = u32x4{pack2<T>(sacc[b][r0 + 0], sacc[b][r0 + 1]), pack2<T>(sacc[b][r0 + 2], sacc[b][r0 + 3]),
-                                    pack2<T>(sacc[b][r0 + 4], sacc[b][r0 + 5]), pack2<T>(sacc[b][r0 + 6], sacc[b][r0 + 7])};
+          const u32x4 pfrag =
+              u32x4{pack2<T>(cur.s[b][r0 + 0], cur.s[b][r0 + 1]), pack2<T>(cur.s[b][r0 + 2], cur.s[b][r0 + 3]),
+                    pack2<T>(cur.s[b][r0 + 4], cur.s[b][r0 + 5]), pack2<T>(cur.s[b][r0 + 6], cur.s[b][r0 + 7])};
           const uint16_t* vrow = vt + n * kVt + (2 * b + u) * 16 + 8 * h;
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt) oacc[dt] = Mfma<T>::m32x32x16(ld16(vrow + 32 * dt * kVt), pfrag, oacc[dt]);
         }
     }
 
-    if (it + 1 < ntiles) store_tile(lds + ((it + 1) & 1) * kBufElems, regs, kv0 + kBN, kv_end, tid);
+    // 3. stage K(it+2) over K(it) and V(it+1) over V(it-1); both were last read before the previous
+    //    barrier.  Then issue the global loads of K(it+3) and V(it+2), and the page ids after them.
+    if (it + 2 < ntiles) store_k(kbuf0 + (it & 1) * kKsElems, kr, kv0 + 2 * kBN, kv_end, tid);
+    if (it + 1 < ntiles) store_v(vbuf0 + ((it + 1) & 1) * kVtElems, vr, kv0 + kBN, kv_end, tid);
+    if (it + 3 < ntiles) kr = load_k(a, kid_next, kv0 + 3 * kBN, kvh, tid);
+    if (it + 2 < ntiles) vr = load_v(a, vid_next, kv0 + 2 * kBN, kvh, tid);
+    if (it + 4 < ntiles) kid_next = k_ids(a, pages, kv0 + 4 * kBN, last, tid);
+    if (it + 3 < ntiles) vid_next = v_id(a, pages, kv0 + 3 * kBN, last, tid);
     __syncthreads();
+    cur = nxt;
   }
 
   if (!row_valid) return;
@@ -268,8 +320,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int r = 4 * g4;
-      u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
-                       pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
+      const u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
+                             pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
       st8(orow + 32 * dt + 8 * g4 + 4 * h, pk);
     }
 }
@@ -305,6 +357,8 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: q, out and pools need aligned rows");
   MLLM_REQUIRE((int64_t)num_prefill_work * num_kv_heads < (1ll << 31), MLLM_ERR_UNSUPPORTED,
                "mllm_paged_prefill: too many work items");
+  MLLM_REQUIRE(num_kv_heads * head_dim * 2 < (1 << 24) && (int64_t)block_size * num_kv_heads * head_dim * 2 < (1ll << 32),
+               MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: KV block too large");
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_tok;
@@ -312,6 +366,8 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   a.kc = static_cast<const uint16_t*>(k_cache);
   a.vc = static_cast<const uint16_t*>(v_cache);
   a.num_blocks = num_blocks;
+  a.row_bytes = num_kv_heads * head_dim * 2;
+  a.page_bytes = (unsigned)((int64_t)block_size * a.row_bytes);
   a.bs = block_size;
   a.bs_shift = __builtin_ctz((unsigned)block_size);
   a.H = num_heads;
