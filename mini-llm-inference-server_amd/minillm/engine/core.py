@@ -1,0 +1,194 @@
+"""Engine core: scheduler + paged pool + model, one unit of GPU work per step
+(reference src/minillm/engine/core.py:56-180; IPC, HTTP and text live outside this package).
+
+`step()`: schedule -> build the step's AttentionMetadata on the GPU (shared by every layer) -> one
+model forward over the ragged new tokens with the pool -> greedy argmax of each sequence's last
+token -> bookkeeping.  The attention backend is whatever the model was built with (`hip` by default).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from ..attention.metadata import AttentionMetadata, SeqStep
+from ..cache.paged import BLOCK_SIZE, PagedKVCache
+from ..cache.prefix import PrefixCache, root_hash
+from .block_manager import BlockManager
+from .scheduler import Request, Scheduler
+
+DEFAULT_MAX_NUM_BATCHED_TOKENS = 8192
+
+
+@dataclass
+class AddRequest:
+    req_id: str
+    prompt_token_ids: list[int]
+    max_tokens: int
+    stop_token_ids: list[int] = field(default_factory=list)
+    ignore_eos: bool = False
+    timeline: dict = field(default_factory=dict)
+    cache_salt: str = ""
+
+
+@dataclass
+class RequestOutput:
+    req_id: str
+    new_token_ids: list[int]
+    finished: bool = False
+    finish_reason: str | None = None
+    timeline: dict | None = None
+    num_prompt_tokens: int = 0
+    num_output_tokens: int = 0
+    num_cached_tokens: int = 0
+
+
+@dataclass
+class EngineStats:
+    num_waiting: int
+    num_running: int
+    kv_tokens_used: int
+    kv_blocks_used: int = 0
+    kv_blocks_total: int = 0
+    num_preemptions: int = 0
+    kv_blocks_cached: int = 0
+    prefix_cache_queries: int = 0
+    prefix_cache_hits: int = 0
+
+
+@dataclass
+class StepOutputs:
+    outputs: list[RequestOutput]
+    stats: EngineStats
+
+
+@dataclass
+class StepRecord:
+    step: int
+    t_start: int
+    duration_ns: int
+    num_seqs: int
+    prefill_tokens: int
+    decode_tokens: int
+    kv_tokens_used: int
+    queue_len: int
+    kv_blocks_used: int = 0
+    num_preempted: int = 0
+
+
+def now_ns() -> int:
+    return time.monotonic_ns()
+
+
+class EngineCore:
+    def __init__(self, model, max_model_len: int | None = None, step_log: bool = False, max_batch_size: int = 1,
+                 max_num_batched_tokens: int | None = None, num_kv_blocks: int | None = None,
+                 enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None) -> None:
+        """`metadata_builder(seqs, block_size, device)` defaults to AttentionMetadata.build (the GPU
+        build); a test may pass another implementation of the same contract."""
+        self.model = model
+        self.build_metadata = metadata_builder or AttentionMetadata.build
+        p = next(model.parameters())
+        self.device, self.dtype = p.device, p.dtype
+        self.max_model_len = max_model_len or model.config.max_position_embeddings
+        self.max_batch_size = max_batch_size
+        if num_kv_blocks is None:
+            num_kv_blocks = max_batch_size * -(-self.max_model_len // BLOCK_SIZE)
+        self.cache = PagedKVCache(model.config, num_kv_blocks, self.device, self.dtype)
+        self.prefix = PrefixCache() if enable_prefix_caching else None
+        self.blocks = BlockManager(num_kv_blocks, BLOCK_SIZE, self.prefix)
+        self.scheduler = Scheduler(max_batch_size, max_num_batched_tokens or DEFAULT_MAX_NUM_BATCHED_TOKENS,
+                                   self.blocks, self.prefix)
+        self._salt_keys = {"block_size": BLOCK_SIZE, "kv_dtype": str(self.dtype).removeprefix("torch."),
+                           "layout": "NHD", "model": model_id}
+        self.step_log: list[StepRecord] | None = [] if step_log else None
+        self._step = 0
+        self._aborted: list[RequestOutput] = []
+
+    def add_request(self, msg: AddRequest) -> None:
+        if not msg.prompt_token_ids:
+            raise ValueError("empty prompt")
+        total = len(msg.prompt_token_ids) + msg.max_tokens
+        if total > self.max_model_len:
+            raise ValueError(f"prompt + max_tokens exceeds max_model_len {self.max_model_len}")
+        if self.blocks.blocks_for(total) > self.blocks.num_blocks:
+            raise ValueError(f"prompt + max_tokens needs more KV blocks than the pool has ({self.blocks.num_blocks})")
+        timeline = dict(msg.timeline)
+        timeline["queued"] = now_ns()
+        stop = frozenset() if msg.ignore_eos else frozenset(msg.stop_token_ids)
+        root = root_hash({**self._salt_keys, "salt": msg.cache_salt}) if self.prefix is not None else b""
+        self.scheduler.add(Request(msg.req_id, list(msg.prompt_token_ids), msg.max_tokens, stop, timeline,
+                                   root=root))
+
+    def abort(self, req_id: str) -> None:
+        req = next((r for r in self.scheduler.running if r.req_id == req_id), None)
+        if req is not None:
+            self.scheduler.finish([req])
+        else:
+            req = self.scheduler.remove_waiting(req_id)
+            if req is None:
+                return
+        self._aborted.append(self._finish(req, [], "abort"))
+
+    def has_work(self) -> bool:
+        s = self.scheduler
+        return bool(s.running or s.waiting or self._aborted)
+
+    def stats(self) -> EngineStats:
+        s = self.scheduler
+        return EngineStats(num_waiting=len(s.waiting), num_running=len(s.running),
+                           kv_tokens_used=sum(r.num_cached for r in s.running),
+                           kv_blocks_used=self.blocks.num_blocks - self.blocks.num_free,
+                           kv_blocks_total=self.blocks.num_blocks, num_preemptions=s.num_preemptions,
+                           kv_blocks_cached=self.blocks.num_cached,
+                           prefix_cache_queries=self.prefix.queries if self.prefix else 0,
+                           prefix_cache_hits=self.prefix.hits if self.prefix else 0)
+
+    def check_blocks(self) -> None:
+        self.blocks.check([r.block_ids for r in self.scheduler.running])
+
+    @torch.inference_mode()
+    def step(self) -> StepOutputs:
+        outputs, self._aborted = self._aborted, []
+        t0 = now_ns()
+        plan = self.scheduler.schedule()
+        reqs = plan.prefill or plan.decode
+        if not reqs:
+            return StepOutputs(outputs, self.stats())
+        for r in plan.prefill:
+            r.timeline.setdefault("scheduled", t0)
+        new = [r.uncached() for r in reqs]
+        meta = self.build_metadata([SeqStep(r.num_cached, len(n), r.block_ids) for r, n in zip(reqs, new)],
+                                   BLOCK_SIZE, self.device)
+        ids = torch.tensor([[t for n in new for t in n]], device=self.device)
+        logits = self.model(ids, kv_cache=self.cache.step(meta), last_index=meta.logits_index)
+        tokens = logits[:, -1].argmax(dim=-1).tolist()
+        t_tok = now_ns()
+        done = []
+        for req, token in zip(reqs, tokens):
+            req.num_cached = req.num_tokens
+            req.output.append(token)
+            req.timeline.setdefault("first_token", t_tok)
+            if token in req.stop_ids or len(req.output) >= req.max_tokens:
+                done.append(req)
+                outputs.append(self._finish(req, [token], "stop" if token in req.stop_ids else "length"))
+            else:
+                outputs.append(RequestOutput(req.req_id, [token]))
+        self.scheduler.name_full_blocks(reqs)
+        self.scheduler.finish(done)
+        if self.step_log is not None:
+            st = self.stats()
+            self.step_log.append(StepRecord(self._step, t0, now_ns() - t0, len(reqs),
+                                            sum(len(n) for n in new) if plan.prefill else 0,
+                                            0 if plan.prefill else len(reqs), st.kv_tokens_used, st.num_waiting,
+                                            st.kv_blocks_used, len(plan.preempted)))
+        self._step += 1
+        return StepOutputs(outputs, self.stats())
+
+    def _finish(self, req: Request, new_tokens: list[int], reason: str) -> RequestOutput:
+        req.timeline["finished"] = now_ns()
+        return RequestOutput(req.req_id, new_tokens, finished=True, finish_reason=reason, timeline=req.timeline,
+                             num_prompt_tokens=len(req.prompt), num_output_tokens=len(req.output),
+                             num_cached_tokens=req.num_cached_tokens or 0)

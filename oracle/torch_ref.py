@@ -45,6 +45,16 @@ def write_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.T
     v_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, v.to(v_cache.dtype))
 
 
+class _Converted:
+    """A pool whose gathered rows are converted on the way out (the pool itself is not copied)."""
+
+    def __init__(self, cache: torch.Tensor, conv) -> None:
+        self.cache, self.conv, self.shape = cache, conv, cache.shape
+
+    def __getitem__(self, idx):
+        return self.conv(self.cache[idx])
+
+
 def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torch.Tensor:
     """Reference `paged_torch_ref.py:31-37`: [num_blocks, bs, Hkv, Dh] through tables [B, nb] ->
     [B, Hkv, length, Dh], the first `length` tokens of every row."""
@@ -55,9 +65,20 @@ def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torc
     return tokens.transpose(1, 2)
 
 
-def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta) -> torch.Tensor:
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
+                    compute_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Reference `paged_torch_ref.py:40-74`.  q [N, H, Dh] -> [N, H, Dh]; the step's own k/v must
-    already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`."""
+    already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`.  With `compute_dtype` the
+    gathered context and q are converted to it before SDPA (and the result back to q's dtype): how the
+    oracle runs on a GPU, in float32."""
+    if compute_dtype is not None and compute_dtype != q.dtype:
+        orig = q.dtype
+
+        def conv(t):
+            return t.to(compute_dtype)
+
+        out = paged_attention(conv(q), _Converted(k_cache, conv), _Converted(v_cache, conv), meta)
+        return out.to(orig)
     out = torch.empty_like(q)
     starts, lens, news = meta.query_start_loc, meta.seq_lens, meta.num_new
 

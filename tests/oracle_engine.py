@@ -1,0 +1,38 @@
+"""The oracle as a drop-in attention backend and metadata builder, for end-to-end comparisons of the
+engine on the GPU: same model, same weights, same engine code, only the hot path swapped."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+
+from oracle import torch_ref
+from oracle.metadata import OracleSeq, build_metadata
+
+
+def oracle_metadata(seqs, block_size, device):
+    """The oracle's metadata build, as device tensors with the contract's field names."""
+    om = build_metadata([OracleSeq(s.num_cached, s.num_new, list(s.block_ids)) for s in seqs], block_size)
+    t = {name: torch.from_numpy(getattr(om, name)).to(device) for name in om.TENSOR_FIELDS}
+    return SimpleNamespace(block_size=block_size, query_start_loc=om.query_start_loc, seq_lens=om.seq_lens,
+                           num_new=om.num_new, max_query_len=om.max_query_len, max_seq_len=om.max_seq_len,
+                           num_seqs=om.num_seqs, **t)
+
+
+class OracleBackend:
+    """write_kv + gather/SDPA restated from the reference; attention computed in float32."""
+
+    name = "oracle"
+
+    def __init__(self, compute_dtype=torch.float32) -> None:
+        self.compute_dtype = compute_dtype
+
+    def forward(self, q, k, v, k_cache, v_cache, meta):
+        torch_ref.write_kv(k_cache, v_cache, meta.slot_mapping, k, v)
+        return torch_ref.paged_attention(q, k_cache, v_cache, meta, compute_dtype=self.compute_dtype)
+
+    def prefill(self, q, k, v, key_valid=None, **kwargs):
+        dt = q.dtype
+        c = self.compute_dtype
+        return torch_ref.prefill(q.to(c), k.to(c), v.to(c), key_valid=key_valid).to(dt)
