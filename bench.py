@@ -14,6 +14,7 @@ baseline: the oracle's restatement of the reference torch backend (gather + SDPA
 host's cores on a bounded sample of the same rows.
 
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
+    python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
 """
 
 from __future__ import annotations
@@ -45,6 +46,10 @@ def parse():
     ap.add_argument("--workload", default="decode_256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=16)
+    ap.add_argument("--compare-oracle", action="store_true",
+                    help="engine_8b: also run the engine with the oracle hot path and compare greedy tokens")
+    ap.add_argument("--requests", type=int, default=128)
+    ap.add_argument("--decode-steps", type=int, default=256)
     return ap.parse_args()
 
 
@@ -79,6 +84,86 @@ def cpu_baseline(wl, rows: int):
                       f"{sub.algorithmic_bytes() / t / 1e9:.2f} GB/s on the same algorithmic bytes"}
 
 
+def bench_engine(args):
+    """End-to-end engine on a random-init Llama-3.1-8B (bf16 weights ~ N(0, 0.02), seed 0): `--requests`
+    prompts of 256-2048 random tokens, each decoded greedily for `--decode-steps` tokens, continuously
+    batched (all requests admitted up to 8192 prompt tokens per prefill step), 16-token blocks, pool
+    sized for 90% occupancy.  Reports decode tokens/s over the decode steps (StepRecord durations)."""
+    import torch
+
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+    from minillm.engine.core import AddRequest, EngineCore
+    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
+    from minillm.model.llama import LlamaForCausalLM, random_init_
+
+    dev = torch.device("cuda:0")
+    cfg = LlamaConfig(**LLAMA_3_1_8B)
+    with torch.device("meta"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to_empty(device=dev).to(torch.bfloat16)
+    random_init_(model, std=0.02, seed=0)
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(256, 2049, (args.requests,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
+    blocks = -(-sum(-(-(n + args.decode_steps) // 16) for n in lens) * 10 // 9)
+
+    def run(backend, builder):
+        model.set_backend(backend)
+        core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=args.requests,
+                          num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder)
+        for i, p in enumerate(prompts):
+            core.add_request(AddRequest(f"r{i}", p, args.decode_steps, ignore_eos=True))
+        out, margins, last = {}, {}, {}
+        hook = model.register_forward_hook(lambda mod, a, o: last.__setitem__("l", o))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while core.has_work():
+            step = core.step()
+            top2 = last["l"][:, -1].float().topk(2, dim=-1).values
+            for o, m in zip(step.outputs, (top2[:, 0] - top2[:, 1]).tolist()):
+                out.setdefault(o.req_id, []).extend(o.new_token_ids)
+                margins.setdefault(o.req_id, []).append(m)
+        wall = time.perf_counter() - t0
+        hook.remove()
+        dec = [r for r in core.step_log if r.decode_tokens]
+        pre = [r for r in core.step_log if r.prefill_tokens]
+        stats = {"decode_tokens_per_s": sum(r.decode_tokens for r in dec) / (sum(r.duration_ns for r in dec) * 1e-9),
+                 "decode_steps": len(dec), "prefill_steps": len(pre),
+                 "prefill_tokens_per_s": sum(r.prefill_tokens for r in pre) / (sum(r.duration_ns for r in pre) * 1e-9),
+                 "median_decode_step_ms": statistics.median(r.duration_ns for r in dec) * 1e-6,
+                 "wall_s": wall, "preemptions": core.stats().num_preemptions}
+        del core
+        torch.cuda.empty_cache()
+        return out, margins, stats
+
+    got, _, st = run(get_backend("hip"), AttentionMetadata.build)
+    line = {"metric": "engine decode tokens/s, random-init Llama-3.1-8B, continuous batching", "unit": "tokens/s",
+            "value": round(st["decode_tokens_per_s"], 1), "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+            "data": "synthetic", "config": {"workload": f"engine_8b: {args.requests} requests, prompts U[256,2048], "
+                                                        f"{args.decode_steps} greedy steps, pool {blocks} blocks (90%)"},
+            "engine": {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}}
+    if args.compare_oracle:
+        from oracle_engine import OracleBackend, oracle_metadata
+
+        exp, margins, st_ref = run(OracleBackend(), oracle_metadata)
+        same = sum(got[r] == exp[r] for r in exp)
+        first_div = []
+        for r in exp:
+            for j, (a, b) in enumerate(zip(got[r], exp[r])):
+                if a != b:
+                    first_div.append((j, margins[r][j]))
+                    break
+        line["oracle_comparison"] = {
+            "requests_identical": same, "requests": len(exp),
+            "tokens_identical_before_first_divergence": sum(
+                next((j for j, (a, b) in enumerate(zip(got[r], exp[r])) if a != b), len(exp[r])) for r in exp),
+            "tokens": sum(len(v) for v in exp.values()),
+            "divergence_margins": [round(m, 4) for _, m in first_div],
+            "oracle_decode_tokens_per_s": round(st_ref["decode_tokens_per_s"], 1)}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -93,6 +178,8 @@ def main():
     from minillm.attention.hip_backend import HipBackend
     from minillm.attention.metadata import AttentionMetadata, SeqStep
 
+    if args.workload == "engine_8b":
+        return bench_engine(args)
     dev = torch.device("cuda:0")
     wl = workloads.WORKLOADS[args.workload]()
     q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)

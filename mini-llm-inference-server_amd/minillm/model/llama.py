@@ -33,13 +33,23 @@ class RMSNorm(nn.Module):
 
 
 class RotaryEmbedding(nn.Module):
+    """The frequency table is derived from the config and kept in float32 on every device it is used on
+    (not a module buffer, so casting the model to bf16 never rounds it)."""
+
     def __init__(self, config: LlamaConfig) -> None:
         super().__init__()
-        self.register_buffer("inv_freq", compute_inv_freq(config), persistent=False)
+        self._inv_freq = compute_inv_freq(config)
+        self._on_device: dict[torch.device, torch.Tensor] = {}
+
+    def inv_freq(self, device: torch.device) -> torch.Tensor:
+        t = self._on_device.get(device)
+        if t is None:
+            t = self._on_device[device] = self._inv_freq.to(device)
+        return t
 
     def forward(self, positions: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
         """positions [B, T] -> cos, sin [B, T, Dh]: float32 angles, the half-size table repeated."""
-        ang = positions[..., None].float() * self.inv_freq.float()
+        ang = positions[..., None].float() * self.inv_freq(positions.device)
         ang = torch.cat([ang, ang], dim=-1)
         return ang.cos().to(dtype), ang.sin().to(dtype)
 

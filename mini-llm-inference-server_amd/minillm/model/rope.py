@@ -15,7 +15,7 @@ import torch
 
 def compute_inv_freq(config) -> torch.Tensor:
     dim = config.head_dim
-    exponents = torch.arange(0, dim, 2, dtype=torch.int64).float() / dim
+    exponents = torch.arange(0, dim, 2, dtype=torch.int64, device="cpu").float() / dim
     inv_freq = 1.0 / (config.rope_theta ** exponents)
     sc = config.rope_scaling
     if sc is None:
