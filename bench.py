@@ -15,6 +15,7 @@ host's cores on a bounded sample of the same rows.
 
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
+    python bench.py --workload copy_1gib                      # counter calibration: a 1 GiB device copy
 """
 
 from __future__ import annotations
@@ -164,6 +165,20 @@ def bench_engine(args):
     print(json.dumps(line), flush=True)
 
 
+def copy_calibration():
+    """A plain device copy of 1 GiB, three times: the known-size reference against which rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters are scaled when reporting a kernel's HBM traffic."""
+    import torch
+
+    x = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -180,6 +195,8 @@ def main():
 
     if args.workload == "engine_8b":
         return bench_engine(args)
+    if args.workload == "copy_1gib":
+        return copy_calibration()
     dev = torch.device("cuda:0")
     wl = workloads.WORKLOADS[args.workload]()
     q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
