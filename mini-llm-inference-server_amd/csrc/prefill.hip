@@ -2,10 +2,10 @@
 // rows with several new tokens, causal within the new chunk and aligned bottom-right over the cached
 // prefix; query i of a row with n new tokens and `len` keys sees keys 0 .. len - n + i).
 //
-// One workgroup (4 wavefronts) per (q tile, KV head).  A q tile is 128 / G new tokens of one row,
-// times the G query heads that share the KV head: 128 MFMA rows, 32 per wavefront (rows are
+// One workgroup (8 wavefronts) per (q tile, KV head).  A q tile is 256 / G new tokens of one row,
+// times the G query heads that share the KV head: 256 MFMA rows, 32 per wavefront (rows are
 // token-major: row = token * G + head).  K/V are streamed in tiles of 64 keys gathered through
-// kv_indices into LDS:
+// kv_indices into LDS (two buffers each):
 //   K  as Ks[key][dim]  (row stride 136 elements)
 //   V  as Vt[dim][key'] (row stride  72 elements), key' a permutation inside each 16-key group
 //      (bits 2 and 3 of the key swapped) so that the PV operand of every lane is one 16-byte read.
@@ -16,14 +16,11 @@
 // reduces each row's max and sum inside the lane plus one exchange with lane l ^ 32, and P^T feeds
 // the PV product without leaving its lanes.
 //
-// Software pipeline (one barrier per tile): iteration i issues the score MFMAs of tile i + 1 first,
-// then runs tile i's softmax on the vector ALUs while those MFMAs execute, then tile i's PV MFMAs.
-// K is therefore staged in LDS two tiles ahead and V one tile ahead (two buffers each: K(i+2) is
-// stored over K(i), V(i+1) over V(i-1)), and the global loads for K(i+3) / V(i+2) are in flight
-// during the whole iteration.  Tiles entirely above a wavefront's causal diagonal are skipped; keys
-// past the tile's causal limit are stored to LDS as zeros.  The running max is rescaled lazily (see
-// the softmax below).  The grid is 1-D with the KV head fastest, so with 8 KV heads each XCD
-// (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and keeps that head's
+// The two halves of the workgroup run phase-shifted (see prefill_kernel): one half's matrix phase
+// coincides with the other half's softmax, so every SIMD has an MFMA stream and a vector stream at
+// once.  Tiles entirely above a wavefront's causal diagonal are skipped; keys past the tile's causal
+// limit are stored to LDS as zeros.  The grid is 1-D with the KV head fastest, so with 8 KV heads
+// each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and keeps that head's
 // shared-prefix pages in its own L2.
 #include <math.h>
 
@@ -38,6 +35,7 @@ constexpr int kKs = 136;  // Ks row stride (elements)
 constexpr int kVt = 72;   // Vt row stride (elements)
 constexpr int kKsElems = kBN * kKs;
 constexpr int kVtElems = kHeadDim * kVt;
+constexpr int kQTileRows = 256;  // query rows (token x head of the group) per workgroup: 8 waves x 32
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -165,14 +163,90 @@ __device__ __forceinline__ STile scores(const uint16_t* ks, const u32x4 (&qf)[8]
   return t;
 }
 
+// Softmax of one score tile (online, exp2 domain) -> the bf16/fp16 P^T operands of its PV product.
+// Masks keys past each row's position when the tile reaches past the wavefront's first row; rescales
+// O and l lazily: only when some row's max grew by more than 2^8, otherwise p = 2^((s - m) c) stays
+// below 256, which the fp32 accumulation and the P operand hold as exactly as values below 1.
 template <typename T>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
+__device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x16 (&oacc)[4], float& m_run,
+                                             float& l_run, int kv0, int qp, int wave_qp_lo, int h, float c) {
+  if (kv0 + kBN - 1 > wave_qp_lo) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+        st.s[b][r] = key > qp ? -INFINITY : st.s[b][r];
+      }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, st.s[b][r]), st.s[b][r + 1]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (__any((mx - m_run) * c > 8.f)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2((m_run - m_new) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+    m_run = m_new;
+  }
+  const float mc = m_run * c;
+  float ps = 0.f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(__builtin_fmaf(st.s[b][r], c, -mc));
+      st.s[b][r] = p;
+      ps += p;
+    }
+  ps += __shfl_xor(ps, 32, 64);
+  l_run += ps;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r0 = 8 * u;
+      pf[b][u] = u32x4{pack2<T>(st.s[b][r0 + 0], st.s[b][r0 + 1]), pack2<T>(st.s[b][r0 + 2], st.s[b][r0 + 3]),
+                       pack2<T>(st.s[b][r0 + 4], st.s[b][r0 + 5]), pack2<T>(st.s[b][r0 + 6], st.s[b][r0 + 7])};
+    }
+}
+
+// O^T += V^T . P^T for one tile: 16 MFMAs, the four 32-dim output tiles as independent chains.
+template <typename T>
+__device__ __forceinline__ void pv_tile(const uint16_t* vt, const u32x4 (&pf)[2][2], f32x16 (&oacc)[4], int n,
+                                        int h) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint16_t* vrow = vt + n * kVt + (2 * b + u) * 16 + 8 * h;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) oacc[dt] = Mfma<T>::m32x32x16(ld16(vrow + 32 * dt * kVt), pf[b][u], oacc[dt]);
+    }
+}
+
+// Two wavefront groups of one workgroup, phase-shifted by half an iteration: while group A (waves
+// 0-3) runs its matrix phase, group B (waves 4-7) runs its vector phase, and the next barrier swaps
+// them, so each SIMD (one wave of each group) keeps its matrix pipe and its vector ALU busy together.
+//   matrix phase i : O += V(i) P(i)  and  S(i+1) = K(i+1) Q^T
+//   vector phase   : P(i+1) = softmax(S(i+1)) (group B's vector phase runs half an iteration earlier)
+// Group A also stages K (K(i+2) into the buffer of K(i), then issues the loads of K(i+3)); group B
+// stages V (V(i+1) over V(i-1), loads of V(i+2)), each in its vector phase.  Every buffer is rewritten
+// only after both groups' last read of it, one barrier earlier.
+template <typename T>
+__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kKsElems + 2 * kVtElems];
   uint16_t* const kbuf0 = lds;
   uint16_t* const vbuf0 = lds + 2 * kKsElems;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int grp = wave >> 2;  // 0: matrix phase first, stages K; 1: vector phase first, stages V
+  const int gtid = tid & 255;
   const int kvh = blockIdx.x % a.Hkv;
   const int2 w = a.work[blockIdx.x / a.Hkv];
   const int seq = w.x, t0 = w.y;
@@ -184,12 +258,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int32_t* pages = a.kv_indices + a.kv_indptr[seq];
   const int tpw = 32 / a.G;  // tokens per wavefront
   const int qt_valid = min(a.QT, nn - t0);
-  // keys any row of this workgroup may see
-  const int kv_end = min(len, cached + t0 + qt_valid);
+  const int kv_end = min(len, cached + t0 + qt_valid);  // keys any row of this workgroup may see
   const int last = kv_end - 1;
   const int ntiles = (kv_end + kBN - 1) / kBN;
 
-  // this lane's row
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + wave * tpw + n / a.G;  // new-token index within the row
   const bool row_valid = tok < nn;
@@ -197,9 +269,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int wave_tok_hi = min(t0 + wave * tpw + tpw, nn) - 1;
   const int wave_qp_hi = wave_tok_hi >= t0 + wave * tpw ? cached + wave_tok_hi : -1;  // -1: no valid row
   const int wave_qp_lo = cached + t0 + wave * tpw;  // position of the wavefront's first row
+  const float c = a.scale_log2;
 
-  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7.
-  u32x4 qf[8];
+  u32x4 qf[8];  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7
   {
     const int head = kvh * a.G + (n % a.G);
     const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
@@ -209,7 +281,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
     }
   }
-
   f32x16 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -217,97 +288,49 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // prologue: K(0), K(1), V(0) into LDS; K(2), V(1) in registers; ids of K(3), V(2)
-  {
-    const Regs4 k0 = load_k(a, k_ids(a, pages, 0, last, tid), 0, kvh, tid);
-    const Regs4 v0 = load_v(a, v_id(a, pages, 0, last, tid), 0, kvh, tid);
-    store_k(kbuf0, k0, 0, kv_end, tid);
-    store_v(vbuf0, v0, 0, kv_end, tid);
-    if (ntiles > 1)
-      store_k(kbuf0 + kKsElems, load_k(a, k_ids(a, pages, kBN, last, tid), kBN, kvh, tid), kBN, kv_end, tid);
-  }
+  // prologue: group A stages K(0), K(1) and loads K(2); group B stages V(0) and loads V(1)
   Regs4 kr, vr;
-  if (ntiles > 2) kr = load_k(a, k_ids(a, pages, 2 * kBN, last, tid), 2 * kBN, kvh, tid);
-  if (ntiles > 1) vr = load_v(a, v_id(a, pages, kBN, last, tid), kBN, kvh, tid);
-  KIds kid_next = k_ids(a, pages, 3 * kBN, last, tid);
-  int vid_next = v_id(a, pages, 2 * kBN, last, tid);
+  KIds kid_next;
+  int vid_next = 0;
+  if (grp == 0) {
+    store_k(kbuf0, load_k(a, k_ids(a, pages, 0, last, gtid), 0, kvh, gtid), 0, kv_end, gtid);
+    if (ntiles > 1)
+      store_k(kbuf0 + kKsElems, load_k(a, k_ids(a, pages, kBN, last, gtid), kBN, kvh, gtid), kBN, kv_end, gtid);
+    if (ntiles > 2) kr = load_k(a, k_ids(a, pages, 2 * kBN, last, gtid), 2 * kBN, kvh, gtid);
+    kid_next = k_ids(a, pages, 3 * kBN, last, gtid);
+  } else {
+    store_v(vbuf0, load_v(a, v_id(a, pages, 0, last, gtid), 0, kvh, gtid), 0, kv_end, gtid);
+    if (ntiles > 1) vr = load_v(a, v_id(a, pages, kBN, last, gtid), kBN, kvh, gtid);
+    vid_next = v_id(a, pages, 2 * kBN, last, gtid);
+  }
   __syncthreads();
-  STile cur;
-  if (0 <= wave_qp_hi) cur = scores<T>(kbuf0, qf, n, h);
-  __syncthreads();  // every wavefront has read K(0) before iteration 0 overwrites it with K(2)
+  STile st;
+  u32x4 pf[2][2];
+  if (0 <= wave_qp_hi) {
+    st = scores<T>(kbuf0, qf, n, h);
+    if (grp == 0) softmax_tile<T>(st, pf, oacc, m_run, l_run, 0, qp, wave_qp_lo, h, c);
+  }
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int kv0 = it * kBN;
-    // 1. score MFMAs of the next tile, issued ahead of this tile's softmax
-    STile nxt;
-    if (it + 1 < ntiles && kv0 + kBN <= wave_qp_hi) nxt = scores<T>(kbuf0 + ((it + 1) & 1) * kKsElems, qf, n, h);
-
-    // 2. softmax and PV of this tile
-    if (kv0 <= wave_qp_hi) {  // some key of this tile is visible to some row of this wavefront
-      if (kv0 + kBN - 1 > wave_qp_lo) {  // the tile reaches past the wavefront's first row: causal mask
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-            cur.s[b][r] = key > qp ? -INFINITY : cur.s[b][r];
-          }
+  for (int p = 0; p < 2 * ntiles; ++p) {
+    if ((p & 1) == grp) {  // matrix phase i
+      const int i = p >> 1;
+      if (i * kBN <= wave_qp_hi) pv_tile<T>(vbuf0 + (i & 1) * kVtElems, pf, oacc, n, h);
+      if (i + 1 < ntiles && (i + 1) * kBN <= wave_qp_hi) st = scores<T>(kbuf0 + ((i + 1) & 1) * kKsElems, qf, n, h);
+    } else {  // vector phase: softmax of S(j), then this group's staging duty
+      const int j = (p + 1) >> 1;
+      if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
+      const int i = p >> 1;
+      if (grp == 0) {
+        if (i + 2 < ntiles) store_k(kbuf0 + (i & 1) * kKsElems, kr, (i + 2) * kBN, kv_end, gtid);
+        if (i + 3 < ntiles) kr = load_k(a, kid_next, (i + 3) * kBN, kvh, gtid);
+        if (i + 4 < ntiles) kid_next = k_ids(a, pages, (i + 4) * kBN, last, gtid);
+      } else {
+        if (i + 1 < ntiles) store_v(vbuf0 + ((i + 1) & 1) * kVtElems, vr, (i + 1) * kBN, kv_end, gtid);
+        if (i + 2 < ntiles) vr = load_v(a, vid_next, (i + 2) * kBN, kvh, gtid);
+        if (i + 3 < ntiles) vid_next = v_id(a, pages, (i + 3) * kBN, last, gtid);
       }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, cur.s[b][r]), cur.s[b][r + 1]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Lazy rescale: the running max only moves (and O, l are rescaled) when some row's max grew by
-      // more than 2^8 in the exp2 domain; otherwise p = 2^((s - m) c) stays below 256, which fp32
-      // accumulation and the bf16 P operand hold exactly as well as values below 1.
-      if (__any((mx - m_run) * a.scale_log2 > 8.f)) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2((m_run - m_new) * a.scale_log2);
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
-        m_run = m_new;
-      }
-      const float mc = m_run * a.scale_log2;
-      float ps = 0.f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(__builtin_fmaf(cur.s[b][r], a.scale_log2, -mc));
-          cur.s[b][r] = p;
-          ps += p;
-        }
-      ps += __shfl_xor(ps, 32, 64);
-      l_run += ps;
-
-      const uint16_t* vt = vbuf0 + (it & 1) * kVtElems;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int r0 = 8 * u;
-          const u32x4 pfrag =
-              u32x4{pack2<T>(cur.s[b][r0 + 0], cur.s[b][r0 + 1]), pack2<T>(cur.s[b][r0 + 2], cur.s[b][r0 + 3]),
-                    pack2<T>(cur.s[b][r0 + 4], cur.s[b][r0 + 5]), pack2<T>(cur.s[b][r0 + 6], cur.s[b][r0 + 7])};
-          const uint16_t* vrow = vt + n * kVt + (2 * b + u) * 16 + 8 * h;
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) oacc[dt] = Mfma<T>::m32x32x16(ld16(vrow + 32 * dt * kVt), pfrag, oacc[dt]);
-        }
     }
-
-    // 3. stage K(it+2) over K(it) and V(it+1) over V(it-1); both were last read before the previous
-    //    barrier.  Then issue the global loads of K(it+3) and V(it+2), and the page ids after them.
-    if (it + 2 < ntiles) store_k(kbuf0 + (it & 1) * kKsElems, kr, kv0 + 2 * kBN, kv_end, tid);
-    if (it + 1 < ntiles) store_v(vbuf0 + ((it + 1) & 1) * kVtElems, vr, kv0 + kBN, kv_end, tid);
-    if (it + 3 < ntiles) kr = load_k(a, kid_next, kv0 + 3 * kBN, kvh, tid);
-    if (it + 2 < ntiles) vr = load_v(a, vid_next, kv0 + 2 * kBN, kvh, tid);
-    if (it + 4 < ntiles) kid_next = k_ids(a, pages, kv0 + 4 * kBN, last, tid);
-    if (it + 3 < ntiles) vid_next = v_id(a, pages, kv0 + 3 * kBN, last, tid);
     __syncthreads();
-    cur = nxt;
   }
 
   if (!row_valid) return;
@@ -346,7 +369,8 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
                "mllm_paged_prefill: num_heads must be a multiple of num_kv_heads");
   const int G = num_heads / num_kv_heads;
   MLLM_REQUIRE(32 % G == 0, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: H / Hkv must divide 32");
-  MLLM_REQUIRE(q_tile_tokens == 128 / G, MLLM_ERR_INVALID, "mllm_paged_prefill: q_tile_tokens must be 128 / (H / Hkv)");
+  MLLM_REQUIRE(q_tile_tokens == kQTileRows / G, MLLM_ERR_INVALID,
+               "mllm_paged_prefill: q_tile_tokens must be 256 / (H / Hkv)");
   MLLM_REQUIRE(num_prefill_work >= 0, MLLM_ERR_INVALID, "mllm_paged_prefill: negative count");
   if (num_prefill_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && prefill_work,
@@ -386,8 +410,8 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
   if (dtype == MLLM_DTYPE_BF16)
-    prefill_kernel<BF16><<<grid, 256, 0, st>>>(a);
+    prefill_kernel<BF16><<<grid, 512, 0, st>>>(a);
   else
-    prefill_kernel<F16><<<grid, 256, 0, st>>>(a);
+    prefill_kernel<F16><<<grid, 512, 0, st>>>(a);
   return check_launch("mllm_paged_prefill");
 }

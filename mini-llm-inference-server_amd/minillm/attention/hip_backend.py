@@ -155,7 +155,7 @@ class HipBackend(AttentionBackend):
         decode_pages = sum(p for p, nn in zip(pages, news) if nn == 1)
         c = pages_per_split(decode_pages, hkv)
         g = h // hkv
-        q_tile = 128 // g if 32 % g == 0 else 1
+        q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
         n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
         n_merge = sum(1 for p, nn in zip(pages, news) if nn == 1 and p > c)
         n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
