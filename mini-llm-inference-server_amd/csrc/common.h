@@ -33,6 +33,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -142,6 +144,32 @@ struct Mfma<F16> {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// acc + lo + hi of a packed pair (v_dot2c_f32_{bf16,f16} against (1, 1)): the pair's own rounded values,
+// summed in fp32.
+template <typename T>
+__device__ __forceinline__ float add_pair(uint32_t packed, float acc);
+template <>
+__device__ __forceinline__ float add_pair<BF16>(uint32_t packed, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), __builtin_bit_cast(bf16x2, 0x3f803f80u),
+                                         acc, false);
+}
+template <>
+__device__ __forceinline__ float add_pair<F16>(uint32_t packed, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, 0x3c003c00u), acc,
+                                false);
+}
+
+// Reductions of lane l with lane l ^ 32 (v_permlane32_swap: the two halves of the wavefront exchange
+// values in the VALU, no LDS round trip).  Both lanes of a pair get the same bits.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 

@@ -4,24 +4,28 @@
 //
 // One workgroup (8 wavefronts) per (q tile, KV head).  A q tile is 256 / G new tokens of one row,
 // times the G query heads that share the KV head: 256 MFMA rows, 32 per wavefront (rows are
-// token-major: row = token * G + head).  K/V are streamed in tiles of 64 keys gathered through
-// kv_indices into LDS (two buffers each):
-//   K  as Ks[key][dim]  (row stride 136 elements)
-//   V  as Vt[dim][key'] (row stride  72 elements), key' a permutation inside each 16-key group
-//      (bits 2 and 3 of the key swapped) so that the PV operand of every lane is one 16-byte read.
+// token-major: row = token * G + head).  K and V stream through LDS in tiles of 64 keys, gathered
+// through kv_indices by direct global->LDS loads (global_load_lds_dwordx4: no VGPR staging) into two
+// rings, K four tiles deep and V three, so each tile's loads are issued four phases before its first
+// use.  A tile in LDS is its 64 key rows of the head, 256 bytes each, with the 16-byte chunks of row r
+// XOR-swizzled (K: chunk ^ (r % 16); V: chunk ^ 4 (r % 4)) so that the MFMA operand reads below hit
+// distinct banks.
 // Per wavefront and K/V tile:
-//   S^T[64 keys x 32 rows] = K . Q^T     2 x 8 v_mfma_f32_32x32x16 (Q^T held in VGPRs for the whole row)
-//   O^T[128 x 32 rows]    += V^T . P^T   4 x 4 v_mfma_f32_32x32x16
+//   S^T[64 keys x 32 rows] = K . Q^T     2 x 8 v_mfma_f32_32x32x16 (K rows by ds_read_b128; Q^T in VGPRs)
+//   O^T[128 x 32 rows]    += V^T . P^T   4 x 4 v_mfma_f32_32x32x16 (V^T by ds_read_b64_tr_b16, the LDS
+//                                         transpose read: 4 consecutive keys of one dim per lane)
 // S^T and P^T share a lane layout (lane l: row l % 32), so the online softmax (fp32, exp2 domain)
 // reduces each row's max and sum inside the lane plus one exchange with lane l ^ 32, and P^T feeds
-// the PV product without leaving its lanes.
+// the PV product without leaving its lanes.  P^T's 16-key k-order is keys {4h..4h+3, 8+4h..8+4h+3}
+// (lane half h); the V^T reads pick their keys in the same order.
 //
 // The two halves of the workgroup run phase-shifted (see prefill_kernel): one half's matrix phase
 // coincides with the other half's softmax, so every SIMD has an MFMA stream and a vector stream at
-// once.  Tiles entirely above a wavefront's causal diagonal are skipped; keys past the tile's causal
-// limit are stored to LDS as zeros.  The grid is 1-D with the KV head fastest, so with 8 KV heads
-// each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and keeps that head's
-// shared-prefix pages in its own L2.
+// once.  Tiles entirely above a wavefront's causal diagonal are skipped.  Keys past the workgroup's
+// last visible key are loaded as copies of that key's row (their scores are masked, so P is exactly
+// 0 and pool slots past a row's length are never read).  The grid is 1-D with the KV head fastest,
+// so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and
+// keeps that head's shared-prefix pages in its own L2.
 #include <math.h>
 
 #include "common.h"
@@ -30,11 +34,14 @@ namespace mllm {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kBN = 64;   // keys per K/V tile
-constexpr int kKs = 136;  // Ks row stride (elements)
-constexpr int kVt = 72;   // Vt row stride (elements)
-constexpr int kKsElems = kBN * kKs;
-constexpr int kVtElems = kHeadDim * kVt;
+constexpr int kBN = 64;                      // keys per K/V tile
+constexpr int kRowBytes = kHeadDim * 2;      // one key row of the head in LDS
+constexpr int kTileBytes = kBN * kRowBytes;  // 16 KB
+constexpr int kRingK = 4;                    // K tiles in LDS
+constexpr int kRingV = 3;                    // V tiles in LDS
+constexpr int kVBase = kRingK * kTileBytes;  // byte offset of the V ring
+constexpr int kIdBase = (kRingK + kRingV) * kTileBytes;  // per wavefront two 64-entry windows of block ids
+constexpr int kLdsBytes = kIdBase + 8 * 2 * 64 * 4;
 constexpr int kQTileRows = 256;  // query rows (token x head of the group) per workgroup: 8 waves x 32
 
 struct PrefillArgs {
@@ -57,108 +64,111 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
 };
 
-// Key position -> position inside the permuted Vt row: within each 16-key group swap bits 2 and 3.
-__device__ __forceinline__ int vt_pos(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
+// ---------------------------------------------------------------- K/V tile loads
+// A 64-key tile is four 16-key groups; a block size is a power of two >= 16, so each group lies in
+// one block.  Wavefront w loads tile rows 8 w .. 8 w + 7 (group w / 2) with two DMA instructions of 4
+// rows each: lane l writes LDS bytes 16 l .. 16 l + 15 of its instruction's 1 KB, i.e. row
+// 8 w + 4 a + l / 16, physical chunk l % 16, and so fetches the logical chunk that the swizzle puts
+// there.  The group's block id is wave-uniform (a scalar load); for a full tile the address is a
+// 64-bit scalar base plus a per-lane offset that never changes.
 
-// Page ids are loaded without branches (a key past the causal limit reads the id of the limit's
-// page), so the compiler never waits on them early; validity is applied when a tile is stored.
-// Thread tid handles K keys tid / 16 + 16 j (j < 4), dims 8 (tid % 16) .. +7, and V keys
-// 4 (tid % 16) .. +3, dims 8 (tid / 16) .. +7.
-struct KIds {
-  int b[4];
-};
+__device__ __forceinline__ int group_block(const PrefillArgs& a, const int32_t* pages, int key0, int last) {
+  return pages[min(key0, last) >> a.bs_shift];
+}
 
-__device__ __forceinline__ KIds k_ids(const PrefillArgs& a, const int32_t* pages, int kv0, int last, int tid) {
-  KIds ids;
+// Pool address of slot key0 % bs of block `id` for this head's rows (uniform).
+__device__ __forceinline__ const char* group_base(const char* pool, const PrefillArgs& a, int id, int key0) {
+  const unsigned b = ((unsigned)id < (unsigned)a.num_blocks) ? (unsigned)id : 0u;  // else-branch never taken
+  return pool + ((uint64_t)b * a.page_bytes + (unsigned)(key0 & (a.bs - 1)) * (unsigned)a.row_bytes);
+}
+
+// Logical chunk fetched by lane l for tile row r (the inverse of the LDS swizzle; XOR is its own inverse).
+__device__ __forceinline__ int k_chunk(int r, int lane) { return (lane & 15) ^ (r & 15); }
+__device__ __forceinline__ int v_chunk(int r, int lane) { return (lane & 15) ^ (4 * (r & 3)); }
+
+__device__ __forceinline__ unsigned lds_offset(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// One DMA instruction (global_load_lds_dword{x4}): lane l's 16 (4) bytes at base + voff land at LDS
+// byte lds + 16 l (4 l).  base and lds are wave-uniform.  Issued from asm, so the compiler neither
+// counts these loads nor waits for them: every wait on them is an explicit vmcnt in a barrier below.
+__device__ __forceinline__ void dma16(const char* base, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4(const char* base, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+
+// This wavefront's share (rows 8 w .. 8 w + 7) of the K or V tile starting at key kv0 into `slot`.
+// off0 / off1: the lanes' offsets from the group base for full tiles; IS_V selects the swizzle.
+template <bool IS_V>
+__device__ __forceinline__ void dma_tile(const char* pool, const PrefillArgs& a, int blk, int kv0, int last,
+                                         int kv_end, int w, unsigned off0, unsigned off1, unsigned head_bytes,
+                                         int lane, char* slot) {
+  const unsigned dst = lds_offset(slot) + 8 * w * kRowBytes;
+  if (kv0 + kBN <= kv_end) {
+    const char* base = group_base(pool, a, blk, kv0 + 16 * (w >> 1));
+    dma16(base, off0, dst);
+    dma16(base, off1, dst + 4 * kRowBytes);
+  } else {  // a row's last tile: keys past `last` load the row of `last` (same block, P = 0)
+    const char* base = group_base(pool, a, blk, 0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ids.b[j] = pages[(unsigned)min(kv0 + tid / 16 + 16 * j, last) >> a.bs_shift];
-  return ids;
-}
-
-__device__ __forceinline__ int v_id(const PrefillArgs& a, const int32_t* pages, int kv0, int last, int tid) {
-  return pages[(unsigned)min(kv0 + 4 * (tid & 15), last) >> a.bs_shift];
-}
-
-// pool + block * page_bytes + slot * row_bytes + col_bytes (slot < block_size and row_bytes < 2^24, so
-// the in-page product is a 24-bit multiply).
-__device__ __forceinline__ const char* row_ptr(const char* pool, const PrefillArgs& a, int blk, int slot,
-                                               int col_bytes) {
-  const unsigned b = ((unsigned)blk < (unsigned)a.num_blocks) ? (unsigned)blk : 0u;  // else-branch never taken
-  const unsigned in_page = __umul24((unsigned)slot, (unsigned)a.row_bytes) + (unsigned)col_bytes;
-  return pool + ((uint64_t)b * a.page_bytes + in_page);
-}
-
-struct Regs4 {
-  u32x4 x[4];
-};
-
-// Global loads of one tile (issued unconditionally; rows past the causal limit come from a valid slot
-// and are zeroed when stored).
-__device__ __forceinline__ Regs4 load_k(const PrefillArgs& a, const KIds& ids, int kv0, int kvh, int tid) {
-  Regs4 r;
-  const char* kc = reinterpret_cast<const char*>(a.kc);
-  const int col = kvh * kHeadDim * 2 + 16 * (tid & 15);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) r.x[j] = ld16(row_ptr(kc, a, ids.b[j], (kv0 + tid / 16 + 16 * j) & (a.bs - 1), col));
-  return r;
-}
-
-__device__ __forceinline__ Regs4 load_v(const PrefillArgs& a, int id, int kv0, int kvh, int tid) {
-  Regs4 r;
-  const char* vp = row_ptr(reinterpret_cast<const char*>(a.vc), a, id, (kv0 + 4 * (tid & 15)) & (a.bs - 1),
-                           kvh * kHeadDim * 2 + 16 * (tid >> 4));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.x[i] = ld16(vp + i * a.row_bytes);
-  return r;
-}
-
-// LDS stores of one tile; keys at or past kv_end become zeros (only a row's last tile has any).
-__device__ __forceinline__ void store_k(uint16_t* ks, Regs4 r, int kv0, int kv_end, int tid) {
-  if (kv0 + kBN > kv_end) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) r.x[j] = kv0 + tid / 16 + 16 * j < kv_end ? r.x[j] : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 2; ++i) {
+      const int r = 8 * w + 4 * i + (lane >> 4);
+      const int c = IS_V ? v_chunk(r, lane) : k_chunk(r, lane);
+      const unsigned slot_bytes = (unsigned)(min(kv0 + r, last) & (a.bs - 1)) * (unsigned)a.row_bytes;
+      dma16(base, slot_bytes + head_bytes + 16u * c, dst + 4 * i * kRowBytes);
+    }
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) st16(ks + (tid / 16 + 16 * j) * kKs + 8 * (tid & 15), r.x[j]);
 }
 
-__device__ __forceinline__ void store_v(uint16_t* vt, Regs4 r, int kv0, int kv_end, int tid) {
-  const int kg = tid & 15, dc = tid >> 4;
-  if (kv0 + kBN > kv_end) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.x[i] = kv0 + 4 * kg + i < kv_end ? r.x[i] : u32x4{0, 0, 0, 0};
-  }
-  // this thread holds keys 4kg .. 4kg+3 at dims 8dc .. 8dc+7; write, per dim, the 4 keys as 8 bytes
-  const int pos = vt_pos(4 * kg);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int dw = e >> 1, hf = e & 1;
-    const u32x2 pk =
-        u32x2{pick_halves(r.x[0][dw], hf, r.x[1][dw], hf), pick_halves(r.x[2][dw], hf, r.x[3][dw], hf)};
-    st8(vt + (8 * dc + e) * kVt + pos, pk);
-  }
+// Workgroup barrier that first waits for this wavefront's LDS reads and for all but its N most recent
+// DMA loads (vmcnt retires loads in issue order).  One asm statement: the compiler moves no LDS access
+// across it and does not add the vmcnt(0) drain that __syncthreads' fence would (outstanding DMA
+// loads count as LDS writes to that fence).
+template <int N>
+__device__ __forceinline__ void barrier_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// N = number of DMA instructions issued since the loads that must have landed (0, 2 or 4)
+__device__ __forceinline__ void barrier_vm_n(int n) {
+  if (n >= 4)
+    barrier_vm<4>();
+  else if (n >= 2)
+    barrier_vm<2>();
+  else
+    barrier_vm<0>();
+}
+
+// ---------------------------------------------------------------- MFMA operands from LDS
+
+__device__ __forceinline__ u32x2 ld_tr(const char* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p));
 }
 
 struct STile {
   f32x16 s[2];  // s[b][r]: key 32 b + 8 (r / 4) + 4 h + r % 4 of the tile, row n
 };
 
-// The two 32-key halves are independent accumulation chains; alternating them keeps two MFMAs in
-// flight instead of waiting on each accumulator in turn.
+// kb: this lane's byte offset, in the LDS array, of row n at dims 0-15 step (kk = 0) of the K tile:
+// row 32 b + n adds 8192 b, and dims step kk moves to logical chunk 2 kk + h, which the swizzle turns
+// into a flip of bits 5-7 (kb ^ 32 kk).  The two 32-key halves are independent accumulation chains.
 template <typename T>
-__device__ __forceinline__ STile scores(const uint16_t* ks, const u32x4 (&qf)[8], int n, int h) {
+__device__ __forceinline__ STile scores(const char* lds, unsigned kb, const u32x4 (&qf)[8]) {
   STile t;
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) t.s[b][r] = 0.f;
-  const uint16_t* krow = ks + n * kKs + 8 * h;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
-    const u32x4 k0 = ld16(krow + 16 * kk);
-    const u32x4 k1 = ld16(krow + 32 * kKs + 16 * kk);
-    t.s[0] = Mfma<T>::m32x32x16(k0, qf[kk], t.s[0]);
-    t.s[1] = Mfma<T>::m32x32x16(k1, qf[kk], t.s[1]);
+    const char* p = lds + (kb ^ (32u * kk));
+    t.s[0] = Mfma<T>::m32x32x16(ld16(p), qf[kk], t.s[0]);
+    t.s[1] = Mfma<T>::m32x32x16(ld16(p + 32 * kRowBytes), qf[kk], t.s[1]);
   }
   return t;
 }
@@ -179,12 +189,13 @@ __device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x1
         st.s[b][r] = key > qp ? -INFINITY : st.s[b][r];
       }
   }
-  float mx = -INFINITY;
+  // row max: four independent chains (v_max3), then the other half of the row from lane l ^ 32
+  float m4[4] = {st.s[0][0], st.s[0][1], st.s[0][2], st.s[0][3]};
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, st.s[b][r]), st.s[b][r + 1]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    for (int r = (b == 0 ? 4 : 0); r < 16; ++r) m4[r & 3] = __builtin_fmaxf(m4[r & 3], st.s[b][r]);
+  const float mx = max_xor32(__builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3])));
   if (__any((mx - m_run) * c > 8.f)) {
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2((m_run - m_new) * c);
@@ -194,17 +205,10 @@ __device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x1
     m_run = m_new;
   }
   const float mc = m_run * c;
-  float ps = 0.f;
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(__builtin_fmaf(st.s[b][r], c, -mc));
-      st.s[b][r] = p;
-      ps += p;
-    }
-  ps += __shfl_xor(ps, 32, 64);
-  l_run += ps;
+    for (int r = 0; r < 16; ++r) st.s[b][r] = fast_exp2(__builtin_fmaf(st.s[b][r], c, -mc));
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -213,20 +217,75 @@ __device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x1
       pf[b][u] = u32x4{pack2<T>(st.s[b][r0 + 0], st.s[b][r0 + 1]), pack2<T>(st.s[b][r0 + 2], st.s[b][r0 + 3]),
                        pack2<T>(st.s[b][r0 + 4], st.s[b][r0 + 5]), pack2<T>(st.s[b][r0 + 6], st.s[b][r0 + 7])};
     }
-}
-
-// O^T += V^T . P^T for one tile: 16 MFMAs, the four 32-dim output tiles as independent chains.
-template <typename T>
-__device__ __forceinline__ void pv_tile(const uint16_t* vt, const u32x4 (&pf)[2][2], f32x16 (&oacc)[4], int n,
-                                        int h) {
+  // row sum of the rounded P operand itself (what the PV product weights V by), four chains
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint16_t* vrow = vt + n * kVt + (2 * b + u) * 16 + 8 * h;
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) oacc[dt] = Mfma<T>::m32x32x16(ld16(vrow + 32 * dt * kVt), pf[b][u], oacc[dt]);
+      for (int d = 0; d < 4; ++d) s4[d] = add_pair<T>(pf[b][u][d], s4[d]);
+  l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
+}
+
+// O^T += V^T . P^T for one tile: 16 MFMAs, the four 32-dim output tiles as independent chains.
+// vb: this lane's byte offset, in the LDS array, of its first V^T read (16-key group 0, dims tile 0,
+// keys 4h .. 4h+3); dims tile dt flips bits 6-7 (vb ^ 64 dt), 16-key group u adds 4096 u and the
+// keys 8+4h .. 8+4h+3 add 2048.  Two transpose reads make one operand: 8 keys of one dim per lane.
+template <typename T>
+__device__ __forceinline__ void pv_tile(const char* lds, unsigned vb, const u32x4 (&pf)[2][2], f32x16 (&oacc)[4]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const char* p = lds + (vb ^ (64u * dt)) + 4096 * (2 * b + u);
+        const u32x2 lo = ld_tr(p), hi = ld_tr(p + 2048);
+        oacc[dt] = Mfma<T>::m32x32x16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[b][u], oacc[dt]);
+      }
+}
+
+// One matrix phase with both products (the common case): O += V(i) P(i), then S(i+1) = K(i+1) Q^T, as
+// one sequence of 32 MFMAs whose LDS operands are read kLookahead steps ahead (the wavefront's SIMD
+// partner is in its softmax, so nothing else hides the LDS latency).  Step f < 16: PV with 16-key group
+// f / 4, dims tile f % 4 (two transpose reads); step f >= 16: S with dims step (f - 16) / 2, key half
+// (f - 16) % 2.  sched_barrier keeps the compiler from regrouping the reads next to their MFMAs.
+constexpr int kLookahead = 4;
+
+__device__ __forceinline__ u32x4 matrix_operand(const char* lds, unsigned vb, unsigned kb, int f) {
+  if (f < 16) {
+    const char* p = lds + (vb ^ (64u * (f & 3))) + 4096 * (f >> 2);
+    const u32x2 lo = ld_tr(p), hi = ld_tr(p + 2048);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+  const int g = f - 16;
+  return ld16(lds + (kb ^ (32u * (g >> 1))) + 32 * kRowBytes * (g & 1));
+}
+
+template <typename T>
+__device__ __forceinline__ void matrix_phase(const char* lds, unsigned vb, unsigned kb, const u32x4 (&pf)[2][2],
+                                             f32x16 (&oacc)[4], STile& st, const u32x4 (&qf)[8]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.s[b][r] = 0.f;
+  u32x4 ring[kLookahead + 1];
+#pragma unroll
+  for (int f = 0; f < kLookahead; ++f) ring[f] = matrix_operand(lds, vb, kb, f);
+#pragma unroll
+  for (int f = 0; f < 32; ++f) {
+    if (f + kLookahead < 32) ring[(f + kLookahead) % (kLookahead + 1)] = matrix_operand(lds, vb, kb, f + kLookahead);
+    const u32x4 op = ring[f % (kLookahead + 1)];
+    if (f < 16) {
+      const int u = f >> 2;
+      oacc[f & 3] = Mfma<T>::m32x32x16(op, pf[u >> 1][u & 1], oacc[f & 3]);
+    } else {
+      const int g = f - 16;
+      st.s[g & 1] = Mfma<T>::m32x32x16(op, qf[g >> 1], st.s[g & 1]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // Two wavefront groups of one workgroup, phase-shifted by half an iteration: while group A (waves
@@ -234,19 +293,18 @@ __device__ __forceinline__ void pv_tile(const uint16_t* vt, const u32x4 (&pf)[2]
 // them, so each SIMD (one wave of each group) keeps its matrix pipe and its vector ALU busy together.
 //   matrix phase i : O += V(i) P(i)  and  S(i+1) = K(i+1) Q^T
 //   vector phase   : P(i+1) = softmax(S(i+1)) (group B's vector phase runs half an iteration earlier)
-// Group A also stages K (K(i+2) into the buffer of K(i), then issues the loads of K(i+3)); group B
-// stages V (V(i+1) over V(i-1), loads of V(i+2)), each in its vector phase.  Every buffer is rewritten
-// only after both groups' last read of it, one barrier earlier.
+// Loads: at even phase 2s every wavefront issues its share of V(s+2) (into the slot of V(s-1)) and
+// K(s+3) (into the slot of K(s-1)), both freed by the barrier that ended phase 2s-1; the barrier that
+// ends phase 2s+1 waits for everything but those, so the tiles phase 2s+2 reads (K(s+2), V(s+1)) have
+// landed in every wavefront's share.
 template <typename T>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kKsElems + 2 * kVtElems];
-  uint16_t* const kbuf0 = lds;
-  uint16_t* const vbuf0 = lds + 2 * kKsElems;
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int grp = wave >> 2;  // 0: matrix phase first, stages K; 1: vector phase first, stages V
-  const int gtid = tid & 255;
+  const int grp = wave >> 2;  // 0: matrix phase first; 1: vector phase first
+  const int wu = __builtin_amdgcn_readfirstlane(wave);  // the same index, as a uniform value (load addressing)
   const int kvh = blockIdx.x % a.Hkv;
   const int2 w = a.work[blockIdx.x / a.Hkv];
   const int seq = w.x, t0 = w.y;
@@ -271,6 +329,35 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const int wave_qp_lo = cached + t0 + wave * tpw;  // position of the wavefront's first row
   const float c = a.scale_log2;
 
+  // load lanes: tile rows r0, r1 of this wavefront's two DMA instructions; offsets from the group base
+  const unsigned head_bytes = (unsigned)(kvh * kRowBytes);
+  const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
+  const unsigned rb = (unsigned)a.row_bytes;
+  const unsigned koff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * k_chunk(r0, lane);
+  const unsigned koff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * k_chunk(r1, lane);
+  const unsigned voff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * v_chunk(r0, lane);
+  const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
+  // operand reads (see scores / pv_tile)
+  const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
+  const unsigned vread = (unsigned)(kVBase + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
+
+  const char* kc = reinterpret_cast<const char*>(a.kc);
+  const char* vc = reinterpret_cast<const char*>(a.vc);
+  const int g16 = 16 * (wu >> 1);  // first key of this wavefront's load group within a tile
+  auto k_slot = [&](int t) { return lds + (t & (kRingK - 1)) * kTileBytes; };
+  auto v_slot = [&](int t) { return lds + kVBase + (t % kRingV) * kTileBytes; };
+
+  // Block ids of this wavefront's load group, in windows of 64 tiles DMA'd into LDS (two per
+  // wavefront): entry j of the window holds the id for tile wbase + j.
+  const int* idwin = reinterpret_cast<const int*>(lds + kIdBase) + wu * 128;
+  auto load_ids = [&](int base, int sel) {
+    dma4(reinterpret_cast<const char*>(pages), 4u * (unsigned)(min((base + lane) * kBN + g16, last) >> a.bs_shift),
+         lds_offset(idwin + 64 * sel));
+  };
+  int wbase = 0, wsel = 0;
+  auto blk_of = [&](int t) { return __builtin_amdgcn_readfirstlane(idwin[64 * wsel + t - wbase]); };
+  load_ids(0, 0);
+
   u32x4 qf[8];  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7
   {
     const int head = kvh * a.G + (n % a.G);
@@ -281,6 +368,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
     }
   }
+  // Q and the first id window have landed before any tile load goes out (the empty asm needs the Q
+  // registers, so the compiler's own wait for them is here, not behind the tile loads)
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
+               : "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
   f32x16 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -288,49 +381,66 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // prologue: group A stages K(0), K(1) and loads K(2); group B stages V(0) and loads V(1)
-  Regs4 kr, vr;
-  KIds kid_next;
-  int vid_next = 0;
-  if (grp == 0) {
-    store_k(kbuf0, load_k(a, k_ids(a, pages, 0, last, gtid), 0, kvh, gtid), 0, kv_end, gtid);
-    if (ntiles > 1)
-      store_k(kbuf0 + kKsElems, load_k(a, k_ids(a, pages, kBN, last, gtid), kBN, kvh, gtid), kBN, kv_end, gtid);
-    if (ntiles > 2) kr = load_k(a, k_ids(a, pages, 2 * kBN, last, gtid), 2 * kBN, kvh, gtid);
-    kid_next = k_ids(a, pages, 3 * kBN, last, gtid);
-  } else {
-    store_v(vbuf0, load_v(a, v_id(a, pages, 0, last, gtid), 0, kvh, gtid), 0, kv_end, gtid);
-    if (ntiles > 1) vr = load_v(a, v_id(a, pages, kBN, last, gtid), kBN, kvh, gtid);
-    vid_next = v_id(a, pages, 2 * kBN, last, gtid);
+  // prologue: K(0), V(0), K(1), V(1), K(2); K(0), V(0) and K(1) have landed after the first barrier
+  {
+    const int b0 = blk_of(0);
+    dma_tile<false>(kc, a, b0, 0, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(0));
+    dma_tile<true>(vc, a, b0, 0, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(0));
   }
-  __syncthreads();
+  if (ntiles > 1) {
+    const int b1 = blk_of(1);
+    dma_tile<false>(kc, a, b1, kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(1));
+    dma_tile<true>(vc, a, b1, kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(1));
+  }
+  if (ntiles > 2)
+    dma_tile<false>(kc, a, blk_of(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes,
+                    lane, k_slot(2));
+  barrier_vm_n(2 * (ntiles > 1) + 2 * (ntiles > 2));
+
   STile st;
   u32x4 pf[2][2];
   if (0 <= wave_qp_hi) {
-    st = scores<T>(kbuf0, qf, n, h);
+    st = scores<T>(lds, kread, qf);
     if (grp == 0) softmax_tile<T>(st, pf, oacc, m_run, l_run, 0, qp, wave_qp_lo, h, c);
   }
 
+  int issued = 0;  // DMA instructions of the last even phase
   for (int p = 0; p < 2 * ntiles; ++p) {
-    if ((p & 1) == grp) {  // matrix phase i
-      const int i = p >> 1;
-      if (i * kBN <= wave_qp_hi) pv_tile<T>(vbuf0 + (i & 1) * kVtElems, pf, oacc, n, h);
-      if (i + 1 < ntiles && (i + 1) * kBN <= wave_qp_hi) st = scores<T>(kbuf0 + ((i + 1) & 1) * kKsElems, qf, n, h);
-    } else {  // vector phase: softmax of S(j), then this group's staging duty
-      const int j = (p + 1) >> 1;
-      if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
-      const int i = p >> 1;
-      if (grp == 0) {
-        if (i + 2 < ntiles) store_k(kbuf0 + (i & 1) * kKsElems, kr, (i + 2) * kBN, kv_end, gtid);
-        if (i + 3 < ntiles) kr = load_k(a, kid_next, (i + 3) * kBN, kvh, gtid);
-        if (i + 4 < ntiles) kid_next = k_ids(a, pages, (i + 4) * kBN, last, gtid);
-      } else {
-        if (i + 1 < ntiles) store_v(vbuf0 + ((i + 1) & 1) * kVtElems, vr, (i + 1) * kBN, kv_end, gtid);
-        if (i + 2 < ntiles) vr = load_v(a, vid_next, (i + 2) * kBN, kvh, gtid);
-        if (i + 3 < ntiles) vid_next = v_id(a, pages, (i + 3) * kBN, last, gtid);
+    const int s = p >> 1;
+    if ((p & 1) == 0) {
+      const int vblk = blk_of(s + 2), kblk = blk_of(s + 3);
+      if (s + 4 >= wbase + 64) {  // the next even phase needs tile s + 4: move the window (its DMA goes
+        wsel ^= 1;                // out before this phase's tile loads, so the barrier that waits for
+        wbase = s + 3;            // those older loads covers it)
+        load_ids(wbase, wsel);
+      }
+      issued = 0;
+      if (s + 2 < ntiles) {
+        dma_tile<true>(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(s + 2));
+        issued += 2;
+      }
+      if (s + 3 < ntiles) {
+        dma_tile<false>(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(s + 3));
+        issued += 2;
       }
     }
-    __syncthreads();
+    if ((p & 1) == grp) {  // matrix phase s
+      const unsigned vb = vread + (s % kRingV) * kTileBytes, kb = kread + ((s + 1) & (kRingK - 1)) * kTileBytes;
+      const bool do_pv = s * kBN <= wave_qp_hi, do_s = s + 1 < ntiles && (s + 1) * kBN <= wave_qp_hi;
+      if (do_pv && do_s) {
+        matrix_phase<T>(lds, vb, kb, pf, oacc, st, qf);
+      } else {
+        if (do_pv) pv_tile<T>(lds, vb, pf, oacc);
+        if (do_s) st = scores<T>(lds, kb, qf);
+      }
+    } else {  // vector phase: softmax of S(j)
+      const int j = (p + 1) >> 1;
+      if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
+    }
+    if (p & 1)
+      barrier_vm_n(issued);
+    else
+      barrier_lds();
   }
 
   if (!row_valid) return;
