@@ -23,9 +23,11 @@ OUT_DIR = HERE / "minillm" / "_lib"
 LIB_NAME = "libminillm_hip.so"
 ARCH = os.environ.get("MLLM_OFFLOAD_ARCH", "gfx950")
 
-# no packed FP32; MFMA accumulators in VGPRs (the unified register file) rather than AGPRs, which
-# keeps the attention loops free of accumulator copies between the two register halves
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+# no packed FP32 in any kernel
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# MFMA accumulators in VGPRs (the unified register file) rather than AGPRs keeps the attention loops
+# free of accumulator copies between the two register halves
+FILE_FLAGS = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for name in ("decode.hip", "prefill.hip")}
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall",
                 "-Wno-unused-function"]
 
@@ -38,7 +40,7 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)

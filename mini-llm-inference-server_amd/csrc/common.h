@@ -145,21 +145,6 @@ struct Mfma<F16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// acc + lo + hi of a packed pair (v_dot2c_f32_{bf16,f16} against (1, 1)): the pair's own rounded values,
-// summed in fp32.
-template <typename T>
-__device__ __forceinline__ float add_pair(uint32_t packed, float acc);
-template <>
-__device__ __forceinline__ float add_pair<BF16>(uint32_t packed, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), __builtin_bit_cast(bf16x2, 0x3f803f80u),
-                                         acc, false);
-}
-template <>
-__device__ __forceinline__ float add_pair<F16>(uint32_t packed, float acc) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, 0x3c003c00u), acc,
-                                false);
-}
-
 // Reductions of lane l with lane l ^ 32 (v_permlane32_swap: the two halves of the wavefront exchange
 // values in the VALU, no LDS round trip).  Both lanes of a pair get the same bits.
 __device__ __forceinline__ float max_xor32(float x) {

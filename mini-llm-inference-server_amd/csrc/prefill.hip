@@ -217,14 +217,14 @@ __device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x1
       pf[b][u] = u32x4{pack2<T>(st.s[b][r0 + 0], st.s[b][r0 + 1]), pack2<T>(st.s[b][r0 + 2], st.s[b][r0 + 3]),
                        pack2<T>(st.s[b][r0 + 4], st.s[b][r0 + 5]), pack2<T>(st.s[b][r0 + 6], st.s[b][r0 + 7])};
     }
-  // row sum of the rounded P operand itself (what the PV product weights V by), four chains
+  // row sum in fp32, four chains: plain adds, because the packed bf16 dot instructions do not run
+  // beside MFMAs (each stalls the SIMD partner's matrix phase); the unrounded sum differs from the sum of
+  // the rounded P operand by unbiased bf16 rounding noise only
   float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) s4[d] = add_pair<T>(pf[b][u][d], s4[d]);
+    for (int r = 0; r < 16; ++r) s4[r & 3] += st.s[b][r];
   l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
 }
 
@@ -424,7 +424,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         issued += 2;
       }
     }
-    if ((p & 1) == grp) {  // matrix phase s
+    if ((p & 1) == grp) {  // matrix phase s, at raised wave priority so its MFMAs issue first on the SIMD
+      __builtin_amdgcn_s_setprio(1);
       const unsigned vb = vread + (s % kRingV) * kTileBytes, kb = kread + ((s + 1) & (kRingK - 1)) * kTileBytes;
       const bool do_pv = s * kBN <= wave_qp_hi, do_s = s + 1 < ntiles && (s + 1) * kBN <= wave_qp_hi;
       if (do_pv && do_s) {
@@ -433,6 +434,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         if (do_pv) pv_tile<T>(lds, vb, pf, oacc);
         if (do_s) st = scores<T>(lds, kb, qf);
       }
+      __builtin_amdgcn_s_setprio(0);
     } else {  // vector phase: softmax of S(j)
       const int j = (p + 1) >> 1;
       if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
