@@ -79,6 +79,26 @@ int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_stride_head, c
                    int64_t num_tokens, void* stream);
 
 /*
+ * Rotary embedding fused with the KV append (the step right before the attention path): the model's
+ * RoPE of q and k (reference src/minillm/model/llama.py:58-72, apply_rotary with the "rotate half"
+ * pairing of dims d and d + Dh/2) and write_kv (paged_torch_ref.py:23-28) in one launch:
+ *   q_out[n, h]                   = q[n, h] * cos[n] + rotate_half(q[n, h]) * sin[n]
+ *   k_cache[slot_mapping[n], h']  = k[n, h'] * cos[n] + rotate_half(k[n, h']) * sin[n]
+ *   v_cache[slot_mapping[n], h']  = v[n, h']
+ * cos / sin: [N, Dh] rows of the model's full-width tables (RotaryEmbedding output, dtype `dtype`).
+ * Bit-exact with those torch expressions on 16-bit tensors: each product is rounded to `dtype`, then
+ * the sum.  q/k/v/q_out: [N, heads, Dh] with element strides (tok, head); all buffers share `dtype`
+ * (BF16 or F16), rows 16-byte aligned, head_dim a multiple of 16.  Slots outside [0, num_slots) are
+ * not written.
+ */
+int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+                        int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
+                        int64_t v_stride_head, const void* cos, const void* sin, int64_t cs_stride_tok,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype, void* q_out,
+                        int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_cache, void* v_cache,
+                        int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens, void* stream);
+
+/*
  * Per-step work plan (the analogue of FlashInfer's plan(), which the reference runs once per step:
  * src/minillm/attention/flashinfer_backend.py:44-64).  Built on the GPU from qo_indptr / kv_indptr.
  *   decode rows (num_new == 1): split into chunks of pages_per_split pages; one int4 work item

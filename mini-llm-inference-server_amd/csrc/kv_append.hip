@@ -5,6 +5,8 @@
 // [Hkv, Dh] row (2 KB for 8 x 128 bf16) is written by a run of consecutive threads into one contiguous
 // pool row.  K and V are the two halves of one launch (blockIdx.y).  General path: one element per
 // thread with a round-to-nearest-even conversion, for mixed dtypes or unaligned strides.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mllm {
@@ -138,4 +140,148 @@ extern "C" int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_str
   MLLM_APPEND_CASE(2, 2)
 #undef MLLM_APPEND_CASE
   return fail(MLLM_ERR_UNSUPPORTED, "mllm_kv_append: dtype pair");
+}
+
+// ---------------------------------------------------------------- rotary embedding fused with the append
+// out[d] = x[d] * cos[d] + rotate_half(x)[d] * sin[d], rotate_half(x) = cat(-x[half:], x[:half])
+// (reference src/minillm/model/llama.py:58-72), evaluated the way torch evaluates that expression on
+// 16-bit tensors: each product in fp32 (exact for 16-bit operands) rounded to the tensor dtype, then the
+// sum in fp32 rounded again.  One thread owns dims [8c, 8c + 8) of both halves of one (token, head)
+// row, so each rotation pair stays in the thread; rows are the H query heads (to q_out), then the Hkv
+// key heads (rotated, to the pool at the token's slot), then the Hkv value heads (copied to the pool).
+
+namespace mllm {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float to_f32(uint16_t b) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return bf16_bits_to_f32(b);
+  else
+    return f16_bits_to_f32(b);
+}
+template <typename T>
+__device__ __forceinline__ uint16_t from_f32(float f) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return f32_to_bf16_bits(f);
+  else
+    return f32_to_f16_bits(f);
+}
+// round(round(x c) + round(r s)) in the 16-bit type.  The rounded products pass through an empty asm:
+// for fp16 the compiler narrows these float ops to native half arithmetic and would otherwise fuse the
+// first product into the sum's fma, skipping that product's own rounding.
+template <typename T>
+__device__ __forceinline__ uint16_t rot1(uint16_t x, uint16_t c, float r, uint16_t s) {
+  float a = to_f32<T>(from_f32<T>(to_f32<T>(x) * to_f32<T>(c)));
+  float b = to_f32<T>(from_f32<T>(r * to_f32<T>(s)));
+  asm volatile("" : "+v"(a), "+v"(b));
+  return from_f32<T>(a + b);
+}
+
+union Chunk {
+  u32x4 v;
+  uint16_t e[8];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_append_kernel(
+    const char* __restrict__ q, int64_t q_st, int64_t q_sh, const char* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const char* __restrict__ v, int64_t v_st, int64_t v_sh, const char* __restrict__ cosp,
+    const char* __restrict__ sinp, int64_t cs_st, char* __restrict__ q_out, int64_t qo_st, int64_t qo_sh,
+    char* __restrict__ k_cache, char* __restrict__ v_cache, int64_t num_slots, int32_t H, int32_t Hkv,
+    int32_t half_bytes, int32_t chunks, const int64_t* __restrict__ slots, int64_t num_tokens) {
+  // strides in bytes; one thread = one 16-byte chunk of the first half and its partner in the second
+  const int rows = H + 2 * Hkv;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= num_tokens * rows * chunks) return;
+  const int64_t t = i / ((int64_t)rows * chunks);
+  const int rem = (int)(i - t * rows * chunks);
+  const int row = rem / chunks;
+  const int64_t lo = (int64_t)(rem - row * chunks) * 16;  // byte offset of the chunk in the first half
+  const int64_t row_bytes = 2 * (int64_t)half_bytes;
+  const char* src;
+  char* dst;
+  bool rotate = true;
+  if (row < H) {
+    src = q + t * q_st + row * q_sh;
+    dst = q_out + t * qo_st + row * qo_sh;
+  } else {
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) return;
+    const int kh = row - H;
+    if (kh < Hkv) {
+      src = k + t * k_st + kh * k_sh;
+      dst = k_cache + (slot * Hkv + kh) * row_bytes;
+    } else {
+      src = v + t * v_st + (kh - Hkv) * v_sh;
+      dst = v_cache + (slot * Hkv + kh - Hkv) * row_bytes;
+      rotate = false;
+    }
+  }
+  Chunk x1, x2;
+  x1.v = ld16(src + lo);
+  x2.v = ld16(src + half_bytes + lo);
+  if (rotate) {
+    Chunk c1, c2, s1, s2, o1, o2;
+    const char* cr = cosp + t * cs_st;
+    const char* sr = sinp + t * cs_st;
+    c1.v = ld16(cr + lo);
+    c2.v = ld16(cr + half_bytes + lo);
+    s1.v = ld16(sr + lo);
+    s2.v = ld16(sr + half_bytes + lo);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o1.e[e] = rot1<T>(x1.e[e], c1.e[e], -to_f32<T>(x2.e[e]), s1.e[e]);  // d < half: rotate_half = -x[d + half]
+      o2.e[e] = rot1<T>(x2.e[e], c2.e[e], to_f32<T>(x1.e[e]), s2.e[e]);   // d >= half: rotate_half = x[d - half]
+    }
+    x1 = o1;
+    x2 = o2;
+  }
+  st16(dst + lo, x1.v);
+  st16(dst + half_bytes + lo, x2.v);
+}
+
+}  // namespace
+}  // namespace mllm
+
+extern "C" int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+                                   int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
+                                   int64_t v_stride_head, const void* cos, const void* sin, int64_t cs_stride_tok,
+                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                   void* q_out, int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_cache,
+                                   void* v_cache, int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens,
+                                   void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
+               "mllm_rope_kv_append: dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(num_tokens >= 0 && num_slots >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0,
+               MLLM_ERR_INVALID, "mllm_rope_kv_append: bad sizes");
+  MLLM_REQUIRE(head_dim % 16 == 0, MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: head_dim must be a multiple of 16");
+  if (num_tokens == 0) return MLLM_OK;
+  MLLM_REQUIRE(q && k && v && cos && sin && q_out && k_cache && v_cache && slot_mapping, MLLM_ERR_INVALID,
+               "mllm_rope_kv_append: null pointer");
+  const int64_t strides[] = {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok,
+                             v_stride_head, cs_stride_tok, q_out_stride_tok, q_out_stride_head};
+  bool aligned = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)q_out |
+                  (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
+  for (int64_t s : strides) aligned = aligned && (s * 2) % 16 == 0;
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: rows must be 16-byte aligned");
+  const int chunks = head_dim / 16;  // 16-byte chunks per half row
+  const int64_t total = num_tokens * (num_heads + 2 * num_kv_heads) * chunks;
+  MLLM_REQUIRE(total < (1ll << 40), MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: too many tokens");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  auto launch = [&](auto tag) {
+    using T = decltype(tag);
+    rope_append_kernel<T><<<grid, 256, 0, st>>>(
+        (const char*)q, q_stride_tok * 2, q_stride_head * 2, (const char*)k, k_stride_tok * 2, k_stride_head * 2,
+        (const char*)v, v_stride_tok * 2, v_stride_head * 2, (const char*)cos, (const char*)sin, cs_stride_tok * 2,
+        (char*)q_out, q_out_stride_tok * 2, q_out_stride_head * 2, (char*)k_cache, (char*)v_cache, num_slots,
+        num_heads, num_kv_heads, head_dim, chunks, slot_mapping, num_tokens);
+  };
+  if (dtype == MLLM_DTYPE_BF16)
+    launch(BF16{});
+  else
+    launch(F16{});
+  return check_launch("mllm_rope_kv_append");
 }

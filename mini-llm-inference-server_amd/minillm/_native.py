@@ -31,6 +31,8 @@ SIGNATURES = {
                                            _p]),
     "mllm_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _i32, _i64, _i32, _i32, _p, _i64,
                                       _p]),
+    "mllm_rope_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32, _i32,
+                                           _i32, _i32, _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p]),
     "mllm_plan": (ctypes.c_int, [_p, _p, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
     "mllm_decode_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32]),
     "mllm_paged_decode": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,

@@ -58,6 +58,9 @@ def _ptr(t: torch.Tensor | None) -> int:
 
 class HipBackend(AttentionBackend):
     name = "hip"
+    # The model hands q and k to `forward_rotary` before RoPE when this is set (LlamaAttention checks it),
+    # so the rotation runs in the KV-append launch; False gives the reference call sequence.
+    fuse_rotary = True
 
     def __init__(self) -> None:
         self._lib = _native.lib()
@@ -92,6 +95,35 @@ class HipBackend(AttentionBackend):
         if n != meta.query_start_loc[-1]:
             raise ValueError(f"q has {n} tokens, the metadata describes {meta.query_start_loc[-1]}")
         return tuple(t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+
+    def forward_rotary(self, q, k, v, cos, sin, k_cache, v_cache, meta):
+        """`forward` with the model's RoPE folded in: q and k arrive before the rotation (reference
+        src/minillm/model/llama.py:110 applies it right before the backend call), with the step's
+        cos / sin rows [N, Dh].  One launch rotates q and k, appends the rotated k and v to the pool and
+        writes the rotated q, bit for bit what apply_rotary followed by `forward` produces."""
+        q, k, v = self._check(q, k, v, k_cache, v_cache, meta)
+        q_rot = self.rope_append(q, k, v, cos, sin, k_cache, v_cache, meta)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        self.attend(q_rot, k_cache, v_cache, meta, out)
+        return out
+
+    def rope_append(self, q, k, v, cos, sin, k_cache, v_cache, meta):
+        """Rotary embedding of q and k plus the KV append (`mllm_rope_kv_append`); returns the rotated q."""
+        n, h, dh = q.shape
+        num_blocks, bs, hkv, _ = k_cache.shape
+        if cos.shape != (n, dh) or sin.shape != (n, dh):
+            raise ValueError(f"cos and sin must be [N, Dh] = [{n}, {dh}]")
+        if cos.dtype != q.dtype or sin.dtype != q.dtype or k_cache.dtype != q.dtype:
+            raise ValueError("q, cos, sin and the pools must share one dtype")
+        if cos.stride(-1) != 1 or sin.stride() != cos.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        q_rot = torch.empty((n, h, dh), dtype=q.dtype, device=q.device)
+        self._lib.call("mllm_rope_kv_append", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                       k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos.data_ptr(), sin.data_ptr(),
+                       cos.stride(0), h, hkv, dh, _native.dtype_code(q.dtype), q_rot.data_ptr(), q_rot.stride(0),
+                       q_rot.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks * bs,
+                       meta.slot_mapping.data_ptr(), n, _native.stream_ptr(q.device))
+        return q_rot
 
     def append(self, k, v, k_cache, v_cache, meta) -> None:
         """KV append (reference write_kv, paged_torch_ref.py:23-28): one launch for K and V."""

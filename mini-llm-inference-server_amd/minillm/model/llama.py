@@ -81,13 +81,19 @@ class LlamaAttention(nn.Module):
         q = self.q_proj(x).view(b, t, -1, dh).transpose(1, 2)
         k = self.k_proj(x).view(b, t, -1, dh).transpose(1, 2)
         v = self.v_proj(x).view(b, t, -1, dh).transpose(1, 2)
-        q, k = apply_rotary(q, cos, sin), apply_rotary(k, cos, sin)
         if getattr(kv_cache, "ragged", False):
             # ragged step: one row of every sequence's new tokens -> [N, heads, Dh] views for the backend
             layer = self.layer_idx
-            out = self.backend.forward(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1),
-                                       kv_cache.cache.k[layer], kv_cache.cache.v[layer], kv_cache.meta)
+            pools = (kv_cache.cache.k[layer], kv_cache.cache.v[layer], kv_cache.meta)
+            if getattr(self.backend, "fuse_rotary", False) and b == 1:
+                # the backend rotates q and k itself, in the launch that appends k and v
+                out = self.backend.forward_rotary(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1),
+                                                  cos[0], sin[0], *pools)
+            else:
+                q, k = apply_rotary(q, cos, sin), apply_rotary(k, cos, sin)
+                out = self.backend.forward(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), *pools)
             return self.o_proj(out.reshape(b, t, -1))
+        q, k = apply_rotary(q, cos, sin), apply_rotary(k, cos, sin)
         if kv_cache is not None:
             raise ValueError("only paged ragged caches (PagedStep) are supported")
         out = self.backend.prefill(q, k, v, key_valid=key_valid)

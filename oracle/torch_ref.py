@@ -45,6 +45,28 @@ def write_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.T
     v_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, v.to(v_cache.dtype))
 
 
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """Reference `model/llama.py:58-61`: cat(-x2, x1) of the last dim's halves."""
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat([-x2, x1], dim=-1)
+
+
+def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Reference `model/llama.py:64-72` on the backend's token-major layout: x [N, heads, Dh],
+    cos / sin [N, Dh] broadcast over the heads.  Eager torch ops, so on 16-bit tensors each product
+    and the sum are rounded to the tensor dtype in turn."""
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    return x * cos + rotate_half(x) * sin
+
+
+def rope_then_write_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> torch.Tensor:
+    """The two steps the fused rotary + append replaces: the model's RoPE of q and k
+    (`model/llama.py:110`) and `write_kv` of the rotated k and of v.  Returns the rotated q."""
+    write_kv(k_cache, v_cache, slot_mapping, apply_rotary(k, cos, sin), v)
+    return apply_rotary(q, cos, sin)
+
+
 class _Converted:
     """A pool whose gathered rows are converted on the way out (the pool itself is not copied)."""
 

@@ -142,3 +142,19 @@ def test_teacher_forced_logits_close(hip):
         top2 = y.topk(2, dim=-1).values
         clear = (top2[:, 0] - top2[:, 1]) > 0.5
         assert bool(((x.argmax(-1) == y.argmax(-1)) | ~clear).all())
+
+
+def test_engine_fused_rotary_is_bit_identical(hip):
+    # RoPE folded into the KV-append launch changes no bit of the engine's logits or tokens
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+
+    model = tiny_model(seed=11, dtype=torch.bfloat16)
+    ps = prompts(8, 1, 200, seed=12)
+    kw = dict(max_batch_size=8, num_kv_blocks=300, max_model_len=4096)
+    fused, unfused = get_backend("hip"), get_backend("hip")
+    unfused.fuse_rotary = False
+    assert fused.fuse_rotary
+    a, _ = run_engine(model, fused, AttentionMetadata.build, ps, 16, **kw)
+    b, _ = run_engine(model, unfused, AttentionMetadata.build, ps, 16, **kw)
+    assert a == b  # tokens and logit margins alike

@@ -250,3 +250,78 @@ def test_prefill_key_valid_own_slot_rule():
     allowed = torch.tensor([[[True, False, False], [False, True, False], [False, True, True]]])
     torch.testing.assert_close(out.double(), naive_dense(q, k, v, allowed), atol=1e-6, rtol=1e-6)
     torch.testing.assert_close(out[0, :, 0], v[0, 0, 0].expand(2, 8))
+
+
+# ---------------------------------------------------------------- rotary embedding + append
+
+
+def test_rope_rotates_pairs_by_hand():
+    # Dh = 4: pairs (0, 2) and (1, 3) at angles a and b; a' = a cos - b sin, b' = b cos + a sin
+    a_ang, b_ang = 0.7, -1.3
+    x = torch.tensor([[[1.0, 2.0, 3.0, 4.0]]], dtype=torch.float64)
+    cos = torch.tensor([[math.cos(a_ang), math.cos(b_ang), math.cos(a_ang), math.cos(b_ang)]], dtype=torch.float64)
+    sin = torch.tensor([[math.sin(a_ang), math.sin(b_ang), math.sin(a_ang), math.sin(b_ang)]], dtype=torch.float64)
+    exp = [1 * math.cos(a_ang) - 3 * math.sin(a_ang), 2 * math.cos(b_ang) - 4 * math.sin(b_ang),
+           3 * math.cos(a_ang) + 1 * math.sin(a_ang), 4 * math.cos(b_ang) + 2 * math.sin(b_ang)]
+    got = torch_ref.apply_rotary(x, cos, sin)[0, 0].tolist()
+    assert got == pytest.approx(exp, abs=1e-12)
+
+
+def _angles(n, dh, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(0, 100000, (n,), generator=g).double()
+    inv = 1.0 / (500000.0 ** (torch.arange(0, dh, 2, dtype=torch.float64) / dh))
+    ang = pos[:, None] * inv
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos(), ang.sin()
+
+
+def test_rope_is_a_rotation():
+    # norms of every pair are kept, and rotating back by -angle restores the input
+    n, h, dh = 64, 4, 16
+    x = torch.randn(n, h, dh, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    cos, sin = _angles(n, dh)
+    y = torch_ref.apply_rotary(x, cos, sin)
+    pair_norm = lambda t: t[..., : dh // 2] ** 2 + t[..., dh // 2:] ** 2  # noqa: E731
+    torch.testing.assert_close(pair_norm(y), pair_norm(x), atol=1e-10, rtol=1e-10)
+    torch.testing.assert_close(torch_ref.apply_rotary(y, cos, -sin), x, atol=1e-10, rtol=1e-10)
+
+
+def test_rope_score_depends_only_on_relative_position():
+    # the reference's property test (tests/test_layers.py:75-85): q.k after rotation depends on m - n only
+    dh = 16
+    gen = torch.Generator().manual_seed(2)
+    q = torch.randn(1, 1, dh, dtype=torch.float64, generator=gen)
+    k = torch.randn(1, 1, dh, dtype=torch.float64, generator=gen)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, dh, 2, dtype=torch.float64) / dh))
+
+    def score(m, n):
+        def cs(p):
+            ang = torch.cat([p * inv, p * inv])[None]
+            return ang.cos(), ang.sin()
+
+        return (torch_ref.apply_rotary(q, *cs(m)) * torch_ref.apply_rotary(k, *cs(n))).sum().item()
+
+    assert score(5, 2) == pytest.approx(score(103, 100), abs=1e-9)
+    assert score(7, 7) == pytest.approx(score(0, 0), abs=1e-9)
+    assert score(5, 2) != pytest.approx(score(5, 3), abs=1e-3)
+
+
+def test_rope_then_write_kv_writes_rotated_k_and_plain_v():
+    n, h, hkv, dh, nb, bs = 6, 4, 2, 8, 4, 4
+    gen = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(n, x, dh, generator=gen) for x in (h, hkv, hkv))
+    cos, sin = (t.float() for t in _angles(n, dh))
+    kc, vc = torch.zeros(nb, bs, hkv, dh), torch.zeros(nb, bs, hkv, dh)
+    slots = torch.tensor([13, 2, 7, 0, 15, 9])
+    q_rot = torch_ref.rope_then_write_kv(q, k, v, cos, sin, kc, vc, slots)
+    flat_k, flat_v = kc.view(-1, hkv, dh), vc.view(-1, hkv, dh)
+    for i, s in enumerate(slots.tolist()):
+        # the pair rule on the written row itself: k'[d] = k[d] cos - k[d + half] sin for d < half
+        half = dh // 2
+        exp = k[i, :, :half] * cos[i, :half] - k[i, :, half:] * sin[i, :half]
+        torch.testing.assert_close(flat_k[s, :, :half], exp, atol=1e-6, rtol=1e-6)
+        assert torch.equal(flat_v[s], v[i])
+    assert q_rot.shape == q.shape
+    untouched = sorted(set(range(nb * bs)) - set(slots.tolist()))
+    assert torch.count_nonzero(flat_k[untouched]) == 0 and torch.count_nonzero(flat_v[untouched]) == 0
