@@ -51,6 +51,8 @@ def parse():
                     help="engine_8b: also run the engine with the oracle hot path and compare greedy tokens")
     ap.add_argument("--requests", type=int, default=128)
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--unfused-rotary", action="store_true",
+                    help="engine_8b: RoPE in torch before the backend call instead of in the KV-append launch")
     return ap.parse_args()
 
 
@@ -83,6 +85,45 @@ def cpu_baseline(wl, rows: int):
             "sample": f"first {len(sel)} of {len(wl.seqs)} rows, one layer x {len(times)} reps (median "
                       f"{t * 1e3:.1f} ms), scaled to {LAYERS} layers; effective "
                       f"{sub.algorithmic_bytes() / t / 1e9:.2f} GB/s on the same algorithmic bytes"}
+
+
+def rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v, reps=20):
+    """The step right before attention, per layer: the fused RoPE + KV append launch against the
+    reference sequence (RoPE of q and k in torch, then the KV-append launch), on the workload's tokens
+    taken as pre-RoPE activations at their positions (Llama-3.1-8B rotary table)."""
+    import torch
+
+    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
+    from minillm.model.llama import RotaryEmbedding, apply_rotary
+
+    cos, sin = RotaryEmbedding(LlamaConfig(**LLAMA_3_1_8B))(meta.positions[None], q.dtype)
+    cos, sin = cos[0], sin[0]
+
+    def fused():
+        backend.rope_append(q, k, v, cos, sin, pool_k, pool_v, meta)
+
+    def unfused():
+        qr = apply_rotary(q.transpose(0, 1)[None], cos[None], sin[None])
+        kr = apply_rotary(k.transpose(0, 1)[None], cos[None], sin[None])
+        backend.append(kr[0].transpose(0, 1), v, pool_k, pool_v, meta)
+        return qr
+
+    out = {}
+    for name, fn in (("fused_us", fused), ("torch_rope_then_append_us", unfused)):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = round(a.elapsed_time(b) / reps * 1e3, 2)
+    n = q.shape[0]
+    moved = n * (2 * q.shape[1] + 4 * k.shape[1]) * q.shape[2] * q.element_size() + 2 * cos.numel() * cos.element_size()
+    out["fused_gbps"] = round(moved / (out["fused_us"] * 1e-6) / 1e9, 1)
+    out["tokens"] = n
+    return out
 
 
 def bench_engine(args):
@@ -138,11 +179,14 @@ def bench_engine(args):
         torch.cuda.empty_cache()
         return out, margins, stats
 
-    got, _, st = run(get_backend("hip"), AttentionMetadata.build)
+    hip_backend = get_backend("hip")
+    hip_backend.fuse_rotary = not args.unfused_rotary
+    got, _, st = run(hip_backend, AttentionMetadata.build)
     line = {"metric": "engine decode tokens/s, random-init Llama-3.1-8B, continuous batching", "unit": "tokens/s",
             "value": round(st["decode_tokens_per_s"], 1), "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
             "data": "synthetic", "config": {"workload": f"engine_8b: {args.requests} requests, prompts U[256,2048], "
-                                                        f"{args.decode_steps} greedy steps, pool {blocks} blocks (90%)"},
+                                                        f"{args.decode_steps} greedy steps, pool {blocks} blocks (90%)",
+                                            "rotary": "torch" if args.unfused_rotary else "fused into the KV append"},
             "engine": {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}}
     if args.compare_oracle:
         from oracle_engine import OracleBackend, oracle_metadata
@@ -301,6 +345,7 @@ def main():
         "per_step_shared_ms": {"metadata_build_and_plan": round(meta_plan_ms, 3)},
         "wall_ms_timed_region": round(wall_ms, 2),
     }
+    line["rotary_append"] = rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_rows)
     print(json.dumps(line), flush=True)
