@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--unfused-rotary", action="store_true",
                     help="engine_8b: RoPE in torch before the backend call instead of in the KV-append launch")
+    ap.add_argument("--chunked-prefill", action="store_true",
+                    help="engine_8b: mixed steps (decode rows + prompt chunks under the token budget)")
+    ap.add_argument("--max-num-batched-tokens", type=int, default=8192)
     return ap.parse_args()
 
 
@@ -153,7 +156,8 @@ def bench_engine(args):
     def run(backend, builder):
         model.set_backend(backend)
         core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=args.requests,
-                          num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder)
+                          num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder,
+                          chunked_prefill=args.chunked_prefill, max_num_batched_tokens=args.max_num_batched_tokens)
         for i, p in enumerate(prompts):
             core.add_request(AddRequest(f"r{i}", p, args.decode_steps, ignore_eos=True))
         out, margins, last = {}, {}, {}
@@ -170,7 +174,10 @@ def bench_engine(args):
         hook.remove()
         dec = [r for r in core.step_log if r.decode_tokens]
         pre = [r for r in core.step_log if r.prefill_tokens]
+        generated = sum(len(v) for v in out.values())
         stats = {"decode_tokens_per_s": sum(r.decode_tokens for r in dec) / (sum(r.duration_ns for r in dec) * 1e-9),
+                 "output_tokens_per_s": generated / (sum(r.duration_ns for r in core.step_log) * 1e-9),
+                 "mixed_steps": sum(1 for r in core.step_log if r.decode_tokens and r.prefill_tokens),
                  "decode_steps": len(dec), "prefill_steps": len(pre),
                  "prefill_tokens_per_s": sum(r.prefill_tokens for r in pre) / (sum(r.duration_ns for r in pre) * 1e-9),
                  "median_decode_step_ms": statistics.median(r.duration_ns for r in dec) * 1e-6,
@@ -186,7 +193,9 @@ def bench_engine(args):
             "value": round(st["decode_tokens_per_s"], 1), "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
             "data": "synthetic", "config": {"workload": f"engine_8b: {args.requests} requests, prompts U[256,2048], "
                                                         f"{args.decode_steps} greedy steps, pool {blocks} blocks (90%)",
-                                            "rotary": "torch" if args.unfused_rotary else "fused into the KV append"},
+                                            "rotary": "torch" if args.unfused_rotary else "fused into the KV append",
+                                            "scheduling": (f"chunked prefill, {args.max_num_batched_tokens}-token steps"
+                                                           if args.chunked_prefill else "prefill-first")},
             "engine": {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}}
     if args.compare_oracle:
         from oracle_engine import OracleBackend, oracle_metadata

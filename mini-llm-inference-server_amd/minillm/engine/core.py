@@ -85,9 +85,11 @@ def now_ns() -> int:
 class EngineCore:
     def __init__(self, model, max_model_len: int | None = None, step_log: bool = False, max_batch_size: int = 1,
                  max_num_batched_tokens: int | None = None, num_kv_blocks: int | None = None,
-                 enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None) -> None:
+                 enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None,
+                 chunked_prefill: bool = False) -> None:
         """`metadata_builder(seqs, block_size, device)` defaults to AttentionMetadata.build (the GPU
-        build); a test may pass another implementation of the same contract."""
+        build); a test may pass another implementation of the same contract.  `chunked_prefill` mixes
+        decode rows and prompt chunks in one step under the token budget (see Scheduler)."""
         self.model = model
         self.build_metadata = metadata_builder or AttentionMetadata.build
         p = next(model.parameters())
@@ -100,7 +102,7 @@ class EngineCore:
         self.prefix = PrefixCache() if enable_prefix_caching else None
         self.blocks = BlockManager(num_kv_blocks, BLOCK_SIZE, self.prefix)
         self.scheduler = Scheduler(max_batch_size, max_num_batched_tokens or DEFAULT_MAX_NUM_BATCHED_TOKENS,
-                                   self.blocks, self.prefix)
+                                   self.blocks, self.prefix, chunked_prefill=chunked_prefill)
         self._salt_keys = {"block_size": BLOCK_SIZE, "kv_dtype": str(self.dtype).removeprefix("torch."),
                            "layout": "NHD", "model": model_id}
         self.step_log: list[StepRecord] | None = [] if step_log else None
@@ -154,12 +156,13 @@ class EngineCore:
         outputs, self._aborted = self._aborted, []
         t0 = now_ns()
         plan = self.scheduler.schedule()
-        reqs = plan.prefill or plan.decode
-        if not reqs:
+        rows = plan.rows()
+        if not rows:
             return StepOutputs(outputs, self.stats())
+        reqs = [r for r, _ in rows]
         for r in plan.prefill:
             r.timeline.setdefault("scheduled", t0)
-        new = [r.uncached() for r in reqs]
+        new = [r.uncached()[:n] for r, n in rows]
         meta = self.build_metadata([SeqStep(r.num_cached, len(n), r.block_ids) for r, n in zip(reqs, new)],
                                    BLOCK_SIZE, self.device)
         ids = torch.tensor([[t for n in new for t in n]], device=self.device)
@@ -167,7 +170,10 @@ class EngineCore:
         tokens = logits[:, -1].argmax(dim=-1).tolist()
         t_tok = now_ns()
         done = []
-        for req, token in zip(reqs, tokens):
+        for req, n, token in zip(reqs, new, tokens):
+            if req.num_cached + len(n) < req.num_tokens:  # a prompt chunk short of the end: nothing sampled
+                req.num_cached += len(n)
+                continue
             req.num_cached = req.num_tokens
             req.output.append(token)
             req.timeline.setdefault("first_token", t_tok)
@@ -181,9 +187,9 @@ class EngineCore:
         if self.step_log is not None:
             st = self.stats()
             self.step_log.append(StepRecord(self._step, t0, now_ns() - t0, len(reqs),
-                                            sum(len(n) for n in new) if plan.prefill else 0,
-                                            0 if plan.prefill else len(reqs), st.kv_tokens_used, st.num_waiting,
-                                            st.kv_blocks_used, len(plan.preempted)))
+                                            sum(plan.chunks[r] for r in plan.prefill), len(plan.decode),
+                                            st.kv_tokens_used, st.num_waiting, st.kv_blocks_used,
+                                            len(plan.preempted)))
         self._step += 1
         return StepOutputs(outputs, self.stats())
 

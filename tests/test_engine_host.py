@@ -123,3 +123,102 @@ def test_prefix_cache_refcounts_and_lru():
     bm.check([])
     bm.clear_cache()
     assert bm.num_cached == 0 and len(pc) == 0 and bm.num_free == 4
+
+
+# ---------------------------------------------------------------- chunked prefill (mixed steps)
+
+
+def test_mixed_step_packs_decodes_then_chunks_under_the_budget():
+    s = Scheduler(max_num_seqs=8, max_num_batched_tokens=24, blocks=BlockManager(20, 16), chunked_prefill=True)
+    a, b = req("a", 10), req("b", 40)
+    s.add(a)
+    s.add(b)
+    out = s.schedule()  # a whole, then b's first 14 tokens
+    assert out.decode == [] and out.rows() == [(a, 10), (b, 14)]
+    prefilled(a)  # a sampled its first token
+    b.num_cached += 14
+    c = req("c", 5)
+    s.add(c)
+    out = s.schedule()  # a decodes, b continues with 23 of its remaining 26, c waits for budget
+    assert out.rows() == [(a, 1), (b, 23)] and list(s.waiting) == [c]
+    a.num_cached += 1
+    a.output.append(9)
+    b.num_cached += 23
+    out = s.schedule()  # a decodes, b's last 3 tokens, c admitted whole
+    assert out.rows() == [(a, 1), (b, 3), (c, 5)] and not s.waiting
+    assert all(len(r.block_ids) * 16 >= r.num_cached + out.chunks[r] for r in (a, b, c))
+    s.blocks.check([r.block_ids for r in s.running])
+
+
+def test_mixed_admission_is_fcfs_and_keeps_the_boundary_reserve():
+    s = Scheduler(max_num_seqs=8, max_num_batched_tokens=100, blocks=BlockManager(3, 16), chunked_prefill=True)
+    full = req("full", 16)  # its first sampled token will need a second block
+    s.add(full)
+    assert s.schedule().rows() == [(full, 16)] and s.blocks.num_free == 2
+    prefilled(full)
+    s.add(req("two", 17))  # needs 2 blocks + the reserve for `full`: does not fit
+    s.add(req("one", 3))  # fits, but FCFS does not skip `two`
+    out = s.schedule()
+    assert out.rows() == [(full, 1)] and [r.req_id for r in s.waiting] == ["two", "one"]
+    assert len(full.block_ids) == 2 and s.blocks.num_free == 1
+
+
+def test_mixed_preemption_of_a_request_inside_its_prompt():
+    bm = BlockManager(5, 16)
+    s = Scheduler(max_num_seqs=4, max_num_batched_tokens=20, blocks=bm, chunked_prefill=True)
+    old, long_ = req("old", 16), req("long", 40)
+    s.add(old)
+    s.add(long_)
+    out = s.schedule()  # old whole (16), long (3 blocks) gets 4 tokens; one block stays free for old
+    assert out.rows() == [(old, 16), (long_, 4)] and bm.num_free == 1
+    prefilled(old)
+    long_.num_cached += 4
+    out = s.schedule()  # old crosses a boundary and takes the last block; long continues
+    assert out.preempted == [] and bm.num_free == 0 and out.rows() == [(old, 1), (long_, 19)]
+    old.num_cached += 1
+    old.output.append(9)
+    long_.num_cached += 19
+    old.num_cached = 32  # pretend old filled its second block: its next decode needs a sixth block
+    old.output += [9] * 15
+    out = s.schedule()  # no free block: the newest request (long, mid-prompt) is preempted
+    assert out.preempted == [long_] and long_.num_cached == 0 and list(s.waiting) == [long_]
+    assert out.rows() == [(old, 1)]
+    bm.check([r.block_ids for r in s.running])
+
+
+def test_chunked_engine_tokens_equal_unchunked_on_cpu():
+    # the whole engine on the CPU in float32 with the oracle hot path: prompts split into chunks
+    # across mixed steps give exactly the greedy tokens of whole-prompt prefill steps
+    import torch
+
+    from minillm.engine.core import AddRequest, EngineCore
+    from minillm.model.config import LlamaConfig
+    from minillm.model.llama import LlamaForCausalLM, random_init_
+    from oracle_engine import OracleBackend, oracle_metadata
+
+    cfg = LlamaConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16, rms_norm_eps=1e-5,
+                      rope_theta=10000.0, max_position_embeddings=512)
+    model = LlamaForCausalLM(cfg)
+    random_init_(model, std=0.2, seed=0)
+    model.set_backend(OracleBackend())
+    gen = torch.Generator().manual_seed(1)
+    prompts = [torch.randint(3, 97, (int(n),), generator=gen).tolist() for n in (5, 70, 33, 1, 120, 16)]
+
+    def run(**kw):
+        core = EngineCore(model, max_model_len=512, max_batch_size=4, num_kv_blocks=40, metadata_builder=oracle_metadata,
+                          enable_prefix_caching=False, step_log=True, **kw)
+        for i, p in enumerate(prompts):
+            core.add_request(AddRequest(f"r{i}", p, 12, ignore_eos=True))
+        outs = {}
+        while core.has_work():
+            for o in core.step().outputs:
+                outs.setdefault(o.req_id, []).extend(o.new_token_ids)
+            core.check_blocks()
+        return outs, core
+
+    whole, _ = run()
+    chunked, core = run(chunked_prefill=True, max_num_batched_tokens=24)
+    assert chunked == whole and all(len(v) == 12 for v in whole.values())
+    mixed = [r for r in core.step_log if r.prefill_tokens and r.decode_tokens]
+    assert mixed and max(r.prefill_tokens + r.decode_tokens for r in core.step_log) <= 24

@@ -158,3 +158,20 @@ def test_engine_fused_rotary_is_bit_identical(hip):
     a, _ = run_engine(model, fused, AttentionMetadata.build, ps, 16, **kw)
     b, _ = run_engine(model, unfused, AttentionMetadata.build, ps, 16, **kw)
     assert a == b  # tokens and logit margins alike
+
+
+def test_chunked_prefill_engine_matches_oracle(hip):
+    # mixed steps: prompts cut into chunks under a 96-token budget, decode rows in the same launches
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+
+    model = tiny_model(seed=13)
+    ps = prompts(10, 1, 400, seed=14)
+    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, max_batch_size=8,
+                           num_kv_blocks=400, max_model_len=4096, chunked_prefill=True, max_num_batched_tokens=96,
+                           step_log=True)
+    exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 20, max_batch_size=8, num_kv_blocks=400,
+                        max_model_len=4096)
+    assert_greedy_match(got, exp)
+    mixed = [r for r in core.step_log if r.prefill_tokens and r.decode_tokens]
+    assert mixed and max(r.prefill_tokens + r.decode_tokens for r in core.step_log) <= 96
