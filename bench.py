@@ -16,6 +16,11 @@ host's cores on a bounded sample of the same rows.
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
     python bench.py --workload copy_1gib                      # counter calibration: a 1 GiB device copy
+    python bench.py --kv-dtype fp8                            # the same step on an fp8 (e4m3fn) pool
+
+With --kv-dtype fp8 the pool holds the workload's values cast to e4m3fn (scale 1: the N(0, 1) data is
+well inside e4m3's range) and the step runs the _fp8 entry points; the algorithmic bytes count one
+byte per pool element.
 """
 
 from __future__ import annotations
@@ -56,6 +61,8 @@ def parse():
     ap.add_argument("--chunked-prefill", action="store_true",
                     help="engine_8b: mixed steps (decode rows + prompt chunks under the token budget)")
     ap.add_argument("--max-num-batched-tokens", type=int, default=8192)
+    ap.add_argument("--kv-dtype", choices=["bf16", "fp8"], default="bf16",
+                    help="KV pool format: bf16 (the reference's) or fp8 e4m3fn with per-tensor scales")
     return ap.parse_args()
 
 
@@ -123,7 +130,8 @@ def rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v, reps=20):
         torch.cuda.synchronize()
         out[name] = round(a.elapsed_time(b) / reps * 1e3, 2)
     n = q.shape[0]
-    moved = n * (2 * q.shape[1] + 4 * k.shape[1]) * q.shape[2] * q.element_size() + 2 * cos.numel() * cos.element_size()
+    moved = (n * q.shape[2] * (2 * q.shape[1] * q.element_size() + 2 * k.shape[1] * k.element_size()
+                               + 2 * k.shape[1] * pool_k.element_size()) + 2 * cos.numel() * cos.element_size())
     out["fused_gbps"] = round(moved / (out["fused_us"] * 1e-6) / 1e9, 1)
     out["tokens"] = n
     return out
@@ -157,7 +165,8 @@ def bench_engine(args):
         model.set_backend(backend)
         core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=args.requests,
                           num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder,
-                          chunked_prefill=args.chunked_prefill, max_num_batched_tokens=args.max_num_batched_tokens)
+                          chunked_prefill=args.chunked_prefill, max_num_batched_tokens=args.max_num_batched_tokens,
+                          kv_cache_dtype=torch.float8_e4m3fn if args.kv_dtype == "fp8" else None)
         for i, p in enumerate(prompts):
             core.add_request(AddRequest(f"r{i}", p, args.decode_steps, ignore_eos=True))
         out, margins, last = {}, {}, {}
@@ -195,7 +204,8 @@ def bench_engine(args):
                                                         f"{args.decode_steps} greedy steps, pool {blocks} blocks (90%)",
                                             "rotary": "torch" if args.unfused_rotary else "fused into the KV append",
                                             "scheduling": (f"chunked prefill, {args.max_num_batched_tokens}-token steps"
-                                                           if args.chunked_prefill else "prefill-first")},
+                                                           if args.chunked_prefill else "prefill-first"),
+                                            "kv_dtype": "fp8_e4m3fn (scales 1)" if args.kv_dtype == "fp8" else "bf16"},
             "engine": {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}}
     if args.compare_oracle:
         from oracle_engine import OracleBackend, oracle_metadata
@@ -254,6 +264,11 @@ def main():
     wl = workloads.WORKLOADS[args.workload]()
     q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
     pool_k, pool_v = wl.pool_k.to(dev), wl.pool_v.to(dev)
+    fp8 = args.kv_dtype == "fp8"
+    kv_elem = 1 if fp8 else 2
+    ks = vs = 1.0
+    if fp8:
+        pool_k, pool_v = pool_k.to(torch.float8_e4m3fn), pool_v.to(torch.float8_e4m3fn)
     seqs = [SeqStep(c, n, b) for c, n, b in wl.seqs]
     backend = HipBackend()
 
@@ -271,18 +286,18 @@ def main():
     plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
 
     def step(ev=None):
-        backend.append(k, v, pool_k, pool_v, meta)
+        backend.append(k, v, pool_k, pool_v, meta, ks, vs)
         if plan.num_decode:
             if ev is not None:
                 ev[0].record()
-            backend.run_decode(q, pool_k, pool_v, meta, out)
+            backend.run_decode(q, pool_k, pool_v, meta, out, ks, vs)
             if ev is not None:
                 ev[1].record()
             backend.run_merge(q, meta, out)
         if plan.num_prefill:
             if ev is not None:
                 ev[2].record()
-            backend.run_prefill(q, pool_k, pool_v, meta, out)
+            backend.run_prefill(q, pool_k, pool_v, meta, out, ks, vs)
             if ev is not None:
                 ev[3].record()
 
@@ -306,14 +321,14 @@ def main():
     pf_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0
 
     n_rows = len(wl.seqs)
-    step_bytes = wl.algorithmic_bytes()
+    step_bytes = wl.algorithmic_bytes(kv_elem)
     per_layer_tok_s = wl.num_tokens / (step_ms * 1e-3)
     value = wl.num_tokens / (LAYERS * step_ms * 1e-3)
     if plan.num_decode:
-        dec_bytes = wl.decode_kernel_bytes()
+        dec_bytes = wl.decode_kernel_bytes(kv_elem)
         achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
         traffic = None
-        tfile = ROOT / "profiles" / f"decode_kernel_{wl.name}_traffic.json"
+        tfile = ROOT / "profiles" / f"decode_kernel_{wl.name}{'_fp8' if fp8 else ''}_traffic.json"
         if tfile.exists():
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -342,6 +357,7 @@ def main():
         "config": {"workload": f"{wl.name}: one attention layer of Llama-3.1-8B shape (32/8 heads, d=128, block 16,"
                                f" bf16), {n_rows} rows, {wl.num_tokens} new tokens; step = KV append + paged "
                                f"attention (+ split merge); value = tokens/s scaled to {LAYERS} layers",
+                   "kv_dtype": "fp8_e4m3fn (scales 1)" if fp8 else "bf16",
                    "rows": n_rows, "new_tokens": wl.num_tokens, "context_tokens": sum(wl.lens),
                    "pages_per_split": plan.pages_per_split, "decode_items": plan.num_decode,
                    "prefill_items": plan.num_prefill},
@@ -355,7 +371,7 @@ def main():
         "wall_ms_timed_region": round(wall_ms, 2),
     }
     line["rotary_append"] = rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v)
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_rows)
     print(json.dumps(line), flush=True)
 

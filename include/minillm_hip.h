@@ -176,6 +176,54 @@ int mllm_dense_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st
                          int32_t num_kv_heads, int32_t q_len, int32_t kv_len, int32_t head_dim, float softmax_scale,
                          int32_t dtype, void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, void* stream);
 
+/*
+ * fp8 KV pool.  No counterpart in the reference's code: it is the reference's planned fp8 KV cache
+ * (docs/distributed_inference_plan.md:310, milestone M9b), which halves the bytes decode streams.
+ * The pool has the layout above with one byte per element, OCP float8 e4m3fn (torch.float8_e4m3fn),
+ * and one scale per tensor (per layer, one for K and one for V):
+ *   stored  = e4m3fn(float(x) * (1.0f / scale))   round to nearest even; magnitudes above 464 and
+ *                                                  non-finite inputs store NaN (torch's cast)
+ *   value   = float(stored) * scale
+ * q, k, v, cos, sin and out stay in `dtype` (BF16 or F16).  Attention reads the pool's exact values
+ * (every e4m3fn value is exact in bf16 and fp16), applies k_scale to the scores and v_scale to the
+ * output, and otherwise matches the 16-bit entry points above, with the same shape limits.
+ */
+
+/* KV append into an fp8 pool (write_kv with the quantizing cast); head_dim a multiple of 16, rows
+ * 16-byte aligned.  Bit-exact with torch's (x.float() * (1 / scale)).to(torch.float8_e4m3fn). */
+int mllm_kv_append_fp8(const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                       int64_t v_stride_tok, int64_t v_stride_head, int32_t src_dtype, void* k_cache, void* v_cache,
+                       int64_t num_slots, int32_t num_kv_heads, int32_t head_dim, const int64_t* slot_mapping,
+                       int64_t num_tokens, float k_scale, float v_scale, void* stream);
+
+/* mllm_rope_kv_append into an fp8 pool: the rotated k (rounded to `dtype`) and v are quantized. */
+int mllm_rope_kv_append_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+                            int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
+                            int64_t v_stride_head, const void* cos, const void* sin, int64_t cs_stride_tok,
+                            int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype, void* q_out,
+                            int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_cache, void* v_cache,
+                            int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens, float k_scale,
+                            float v_scale, void* stream);
+
+/* mllm_paged_decode over an fp8 pool; mllm_merge_splits combines its partials unchanged. */
+int mllm_paged_decode_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                          const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                          const int32_t* kv_indices, const int32_t* seq_lens, const int32_t* decode_work,
+                          int32_t num_decode_work, const int32_t* merge_work, int32_t num_merge_work,
+                          int32_t pages_per_split, float softmax_scale, int32_t dtype, float k_scale, float v_scale,
+                          void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/* mllm_paged_prefill over an fp8 pool. */
+int mllm_paged_prefill_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                           const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                           const int32_t* kv_indices, const int32_t* seq_lens, const int32_t* prefill_work,
+                           int32_t num_prefill_work, int32_t q_tile_tokens, float softmax_scale, int32_t dtype,
+                           float k_scale, float v_scale, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,47 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
+// ---------------------------------------------------------------- fp8 KV pool (OCP e4m3fn)
+// 1 sign, 4 exponent (bias 7) and 3 mantissa bits; no infinities, S.1111.111 is NaN; the largest finite
+// magnitude is 448 and the smallest subnormal 2^-9.
+
+struct FP8 {};  // pool storage tag
+
+// float -> e4m3fn bits, round to nearest even on the e4m3 grid (subnormals included).  A magnitude that
+// rounds past 448 (anything above 464), infinity and NaN give NaN with the input's sign: the result of
+// torch's .to(torch.float8_e4m3fn).
+__device__ __forceinline__ uint32_t f32_to_e4m3fn_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x43f00000u) return sign | 0x7fu;  // |f| >= 480, infinity, NaN
+  if (a < 0x3c800000u)                        // |f| < 2^-6: the subnormal grid, steps of 2^-9
+    return sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.f);
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);  // keep 3 mantissa bits, ties to even
+  return sign | ((r - (120u << 23)) >> 20);            // exponent bias 127 -> 7
+}
+
+// Four e4m3fn values (bytes 0-3 of w) -> four bf16 / fp16 values, two per dword, in byte order.  Exact:
+// every e4m3fn value, subnormals and NaN included, is representable in both 16-bit formats.
+template <typename T>
+__device__ __forceinline__ u32x2 fp8x4_to(uint32_t w);
+template <>
+__device__ __forceinline__ u32x2 fp8x4_to<BF16>(uint32_t w) {
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true))};
+}
+template <>
+__device__ __forceinline__ u32x2 fp8x4_to<F16>(uint32_t w) {
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, true))};
+}
+// Eight e4m3fn values (two dwords) -> eight 16-bit values (16 bytes).
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8_to(uint32_t w0, uint32_t w1) {
+  const u32x2 lo = fp8x4_to<T>(w0), hi = fp8x4_to<T>(w1);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
 // Packs two floats into one dword of 16-bit values (lo in bits 0-15), rounding to nearest even with
 // the hardware conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).  For the attention
 // kernels' P tiles and outputs; KV append keeps the bit-level conversion above, whose NaN encoding

@@ -14,6 +14,13 @@
 // assembled with v_perm_b32.  The next 16-token tile is loaded before the current one is consumed.
 // Rows with one chunk write the normalised output; longer rows write fp32 (m, l, acc) partials that a
 // second kernel merges with a log-sum-exp.
+//
+// fp8 (e4m3fn) pools: a tile is half the bytes.  Each lane loads K row (l % 16) as two 16-byte pieces,
+// dims 64 h + 16 (l / 16) .. +15 for h = 0, 1, so S^T's k-dimension runs through the dims in that
+// order (the Q^T operand is loaded in the same order; a dot product does not depend on it), and V rows
+// 4 (l / 16) .. +3 at dims 8 (l % 16) .. +7 as four 8-byte pieces.  The tile is widened to bf16/fp16 in
+// registers (v_cvt_scalef32_pk_*_fp8 with scale 1: exact) right before it is consumed, so the MFMA
+// stream is the 16-bit one; k_scale is folded into the softmax scale and v_scale into the output.
 #include <math.h>
 
 #include "common.h"
@@ -27,8 +34,8 @@ constexpr int kWaves = 4;  // KV heads per workgroup
 struct DecodeArgs {
   const uint16_t* q;
   int64_t q_st, q_sh;
-  const uint16_t* kc;
-  const uint16_t* vc;
+  const char* kc;  // pools, addressed in bytes
+  const char* vc;
   int64_t num_blocks;
   int bs, H, Hkv, G, HG;
   const int32_t* qo_indptr;
@@ -37,7 +44,8 @@ struct DecodeArgs {
   const int32_t* seq_lens;
   const int4* work;
   int C;
-  float scale_log2;
+  float scale_log2;  // softmax scale x k_scale x log2(e)
+  float v_scale;     // output scale of an fp8 pool
   uint16_t* out;
   int64_t o_st, o_sh;
   float* part_o;
@@ -51,24 +59,65 @@ __device__ __forceinline__ u32x4 ldkv(const char* p) {
   else
     return ld16(p);
 }
-
-// Loads 16-token tile t of this wave's page range: K rows in the A layout of S^T = K Q^T (lane (c, g):
-// row c, dims 32 kk + 8 g .. +7) and V rows 4 g .. 4 g + 3 at dims 8 c .. 8 c + 7.
 template <bool NT>
-__device__ __forceinline__ void load_tile(const DecodeArgs& a, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t tok_stride, int64_t blk_stride, int page_lo, int page_hi, int t,
-                                          int tpp, int c, int g, u32x4 (&ka)[4], u32x4 (&va)[4]) {
+__device__ __forceinline__ u32x2 ldkv8(const char* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  else
+    return ld8(p);
+}
+
+// The registers of one loaded 16-token tile, as the pool stores it.
+template <bool F8>
+struct TileRegs {  // 16-bit pool: K row c at dims 32 kk + 8 g .. +7; V rows 4 g + i at dims 8 c .. 8 c + 7
+  u32x4 k[4];
+  u32x4 v[4];
+};
+template <>
+struct TileRegs<true> {  // fp8 pool: K row c at dims 64 h + 16 g .. +15; V rows 4 g + i at dims 8 c .. 8 c + 7
+  u32x4 k[2];
+  u32x2 v[4];
+};
+
+// Dims of the Q^T operand (and of the K operand) that lane group g holds at k-step kk of S^T = K Q^T.
+template <bool F8>
+__device__ __forceinline__ int qk_dim0(int kk, int g) {
+  return F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : 32 * kk + 8 * g;
+}
+
+// Loads 16-token tile t of this wave's page range (lane (c, g); kbase/vbase: this head's bytes of the
+// pools, strides in bytes).
+template <bool F8, bool NT>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, const char* kbase, const char* vbase, int64_t tok_stride,
+                                          int64_t blk_stride, int page_lo, int page_hi, int t, int tpp, int c, int g,
+                                          TileRegs<F8>& r) {
   const int page = t / tpp;
   const int sub = t - page * tpp;
   int blk = __builtin_amdgcn_readlane(page < 64 ? page_lo : page_hi, page & 63);
   if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
   const int64_t off = (int64_t)blk * blk_stride + (int64_t)(sub * 16) * tok_stride;
-  const char* kp = reinterpret_cast<const char*>(kbase + off + c * tok_stride);
+  const char* kp = kbase + off + c * tok_stride;
+  const char* vp = vbase + off + (4 * g) * tok_stride;
+  if constexpr (F8) {
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) ka[kk] = ldkv<NT>(kp + (32 * kk + 8 * g) * 2);
-  const char* vp = reinterpret_cast<const char*>(vbase + off + (4 * g) * tok_stride + 8 * c);
+    for (int h = 0; h < 2; ++h) r.k[h] = ldkv<NT>(kp + 64 * h + 16 * g);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) va[i] = ldkv<NT>(vp + (int64_t)i * tok_stride * 2);
+    for (int i = 0; i < 4; ++i) r.v[i] = ldkv8<NT>(vp + (int64_t)i * tok_stride + 8 * c);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) r.k[kk] = ldkv<NT>(kp + 2 * qk_dim0<false>(kk, g));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.v[i] = ldkv<NT>(vp + (int64_t)i * tok_stride + 16 * c);
+  }
+}
+
+// A loaded fp8 tile as 16-bit MFMA operands: K in the A layout of S^T (k-step kk) and V rows 4 g + i.
+template <typename T>
+__device__ __forceinline__ void widen(const TileRegs<true>& r, u32x4 (&ka)[4], u32x4 (&va)[4]) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ka[kk] = fp8x8_to<T>(r.k[kk >> 1][2 * (kk & 1)], r.k[kk >> 1][2 * (kk & 1) + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) va[i] = fp8x8_to<T>(r.v[i][0], r.v[i][1]);
 }
 
 // One 16-token tile: scores, online-softmax update, PV accumulation.
@@ -117,7 +166,7 @@ __device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4
 }
 
 // PF: tiles loaded ahead of the one being consumed (a ring of PF + 1 register tiles).
-template <typename T, int PF, bool NT, int OCC>
+template <typename T, bool F8, int PF, bool NT, int OCC>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_kernel(
     const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
@@ -156,15 +205,16 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
                                                    (int64_t)(kvh * a.G + (qvalid ? c : 0)) * a.q_sh);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      u32x4 v = ld16(qp + (32 * kk + 8 * g) * 2);
+      u32x4 v = ld16(qp + 2 * qk_dim0<F8>(kk, g));
       qf[kk] = qvalid ? v : u32x4{0, 0, 0, 0};
     }
   }
 
-  const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;
+  constexpr int kElem = F8 ? 1 : 2;  // pool bytes per element
+  const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim * kElem;
   const int64_t blk_stride = (int64_t)a.bs * tok_stride;
-  const uint16_t* kbase = a.kc + kvh * kHeadDim;
-  const uint16_t* vbase = a.vc + kvh * kHeadDim;
+  const char* kbase = a.kc + kvh * kHeadDim * kElem;
+  const char* vbase = a.vc + kvh * kHeadDim * kElem;
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 o[8];
@@ -172,19 +222,25 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   for (int m = 0; m < 8; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   constexpr int R = PF + 1;
-  u32x4 kb[R][4], vb[R][4];
+  TileRegs<F8> ring[R];
 #pragma unroll
   for (int r = 0; r < PF; ++r)
-    if (r < ntiles) load_tile<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, r, tpp, c, g, kb[r], vb[r]);
+    if (r < ntiles) load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, r, tpp, c, g, ring[r]);
   for (int t0 = 0; t0 < ntiles; t0 += R) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int t = t0 + r;
       if (t < ntiles) {
         if (t + PF < ntiles)
-          load_tile<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, t + PF, tpp, c, g,
-                        kb[(r + PF) % R], vb[(r + PF) % R]);
-        consume_tile<T>(kb[r], vb[r], qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+          load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, t + PF, tpp, c, g,
+                            ring[(r + PF) % R]);
+        if constexpr (F8) {
+          u32x4 ka[4], va[4];
+          widen<T>(ring[r], ka, va);
+          consume_tile<T>(ka, va, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+        } else {
+          consume_tile<T>(ring[r].k, ring[r].v, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+        }
       }
     }
   }
@@ -193,7 +249,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   const int head = kvh * a.G + c;
   // lane (c, g) owns dims 32 g + 8 i + m of head c: o[m][i]
   if (nsplit == 1) {
-    const float inv = 1.f / l_run;
+    const float inv = F8 ? a.v_scale / l_run : 1.f / l_run;
     char* op = reinterpret_cast<char*>(a.out + (int64_t)qtok * a.o_st + (int64_t)head * a.o_sh + 32 * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -204,6 +260,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   } else {
     const int64_t row = (int64_t)slot * a.H + head;
     float* po = a.part_o + row * kHeadDim + 32 * g;
+    if constexpr (F8) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) o[m] *= a.v_scale;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       *reinterpret_cast<f32x4*>(po + 8 * i) = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
@@ -244,12 +304,18 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
 constexpr int kPrefetch = 1;
 constexpr bool kNonTemporal = true;
 constexpr int kOccupancy = 3;
+// fp8 tiles hold half the bytes in half the registers: two tiles of lookahead keep as many bytes in
+// flight as one 16-bit tile.
+#ifndef MLLM_DECODE_FP8_PREFETCH
+#define MLLM_DECODE_FP8_PREFETCH 2
+#endif
+constexpr int kPrefetchFp8 = MLLM_DECODE_FP8_PREFETCH;
 
-template <typename T>
+template <typename T, bool F8>
 int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
   const unsigned grid = (unsigned)n_work * (unsigned)a.HG;
-  decode_kernel<T, kPrefetch, kNonTemporal, kOccupancy><<<grid, 64 * kWaves, 0, st>>>(a);
-  return check_launch("mllm_paged_decode");
+  decode_kernel<T, F8, F8 ? kPrefetchFp8 : kPrefetch, kNonTemporal, kOccupancy><<<grid, 64 * kWaves, 0, st>>>(a);
+  return check_launch(F8 ? "mllm_paged_decode_fp8" : "mllm_paged_decode");
 }
 
 }  // namespace
@@ -260,45 +326,50 @@ extern "C" int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t 
   return (int64_t)num_decode_work * num_heads * ((int64_t)head_dim * 4 + 8);
 }
 
-extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+namespace {
+
+int paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                                  const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
                                  int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
                                  const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
                                  const int32_t* decode_work, int32_t num_decode_work, const int32_t* merge_work,
                                  int32_t num_merge_work, int32_t pages_per_split, float softmax_scale, int32_t dtype,
                                  void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
-                                 int64_t workspace_bytes, void* stream) {
+                                 int64_t workspace_bytes, bool fp8, float k_scale, float v_scale, void* stream) {
   using namespace mllm;
+  const std::string fn = fp8 ? "mllm_paged_decode_fp8" : "mllm_paged_decode";
   MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_decode: dtype must be bfloat16 or float16");
-  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode: head_dim must be 128");
+               fn + ": dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, fn + ": head_dim must be 128");
+  MLLM_REQUIRE(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY, MLLM_ERR_INVALID,
+               fn + ": scales must be positive and finite");
   MLLM_REQUIRE(block_size > 0 && block_size % 16 == 0, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_decode: block_size must be a multiple of 16");
+               fn + ": block_size must be a multiple of 16");
   MLLM_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, MLLM_ERR_INVALID,
-               "mllm_paged_decode: num_heads must be a multiple of num_kv_heads");
+               fn + ": num_heads must be a multiple of num_kv_heads");
   MLLM_REQUIRE(num_heads / num_kv_heads <= 16, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_decode: at most 16 query heads per KV head");
+               fn + ": at most 16 query heads per KV head");
   MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
-               "mllm_paged_decode: pages_per_split must be in [1, 128]");
-  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID, "mllm_paged_decode: negative count");
+               fn + ": pages_per_split must be in [1, 128]");
+  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID, fn + ": negative count");
   if (num_decode_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && decode_work,
-               MLLM_ERR_INVALID, "mllm_paged_decode: null pointer");
+               MLLM_ERR_INVALID, fn + ": null pointer");
   const int64_t need = num_merge_work ? mllm_decode_workspace_bytes(num_decode_work, num_heads, head_dim) : 0;
   MLLM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), MLLM_ERR_INVALID,
-               "mllm_paged_decode: workspace too small");
+               fn + ": workspace too small");
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)out % 16 == 0) && ((uintptr_t)k_cache % 16 == 0) &&
                        ((uintptr_t)v_cache % 16 == 0) && (q_stride_tok * 2) % 16 == 0 &&
                        (q_stride_head * 2) % 16 == 0 && (out_stride_tok * 2) % 16 == 0 &&
                        (out_stride_head * 2) % 16 == 0;
-  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode: q, out and pools need 16-byte aligned rows");
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, fn + ": q, out and pools need 16-byte aligned rows");
 
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_tok;
   a.q_sh = q_stride_head;
-  a.kc = static_cast<const uint16_t*>(k_cache);
-  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.kc = static_cast<const char*>(k_cache);
+  a.vc = static_cast<const char*>(v_cache);
   a.num_blocks = num_blocks;
   a.bs = block_size;
   a.H = num_heads;
@@ -311,7 +382,8 @@ extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_
   a.seq_lens = seq_lens;
   a.work = reinterpret_cast<const int4*>(decode_work);
   a.C = pages_per_split;
-  a.scale_log2 = softmax_scale * kLog2e;
+  a.scale_log2 = softmax_scale * k_scale * kLog2e;
+  a.v_scale = v_scale;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
@@ -320,8 +392,38 @@ extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_
                                         (int64_t)num_decode_work * num_heads * head_dim * 4);
   (void)merge_work;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == MLLM_DTYPE_BF16) return launch<BF16>(a, num_decode_work, st);
-  return launch<F16>(a, num_decode_work, st);
+  if (dtype == MLLM_DTYPE_BF16) return fp8 ? launch<BF16, true>(a, num_decode_work, st) : launch<BF16, false>(a, num_decode_work, st);
+  return fp8 ? launch<F16, true>(a, num_decode_work, st) : launch<F16, false>(a, num_decode_work, st);
+}
+
+}  // namespace
+
+extern "C" int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                 const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                                 const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                 const int32_t* decode_work, int32_t num_decode_work, const int32_t* merge_work,
+                                 int32_t num_merge_work, int32_t pages_per_split, float softmax_scale, int32_t dtype,
+                                 void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  return paged_decode(q, q_stride_tok, q_stride_head, k_cache, v_cache, num_blocks, block_size, num_heads,
+                      num_kv_heads, head_dim, qo_indptr, kv_indptr, kv_indices, seq_lens, decode_work, num_decode_work,
+                      merge_work, num_merge_work, pages_per_split, softmax_scale, dtype, out, out_stride_tok,
+                      out_stride_head, workspace, workspace_bytes, false, 1.f, 1.f, stream);
+}
+
+extern "C" int mllm_paged_decode_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                     const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                                     const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                     const int32_t* decode_work, int32_t num_decode_work, const int32_t* merge_work,
+                                     int32_t num_merge_work, int32_t pages_per_split, float softmax_scale,
+                                     int32_t dtype, float k_scale, float v_scale, void* out, int64_t out_stride_tok,
+                                     int64_t out_stride_head, void* workspace, int64_t workspace_bytes, void* stream) {
+  return paged_decode(q, q_stride_tok, q_stride_head, k_cache, v_cache, num_blocks, block_size, num_heads,
+                      num_kv_heads, head_dim, qo_indptr, kv_indptr, kv_indices, seq_lens, decode_work, num_decode_work,
+                      merge_work, num_merge_work, pages_per_split, softmax_scale, dtype, out, out_stride_tok,
+                      out_stride_head, workspace, workspace_bytes, true, k_scale, v_scale, stream);
 }
 
 extern "C" int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work,

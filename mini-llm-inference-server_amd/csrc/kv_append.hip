@@ -5,12 +5,45 @@
 // [Hkv, Dh] row (2 KB for 8 x 128 bf16) is written by a run of consecutive threads into one contiguous
 // pool row.  K and V are the two halves of one launch (blockIdx.y).  General path: one element per
 // thread with a round-to-nearest-even conversion, for mixed dtypes or unaligned strides.
+//
+// fp8 pool (mllm_kv_append_fp8, mllm_rope_kv_append_fp8): each element is stored as
+// e4m3fn(float(x) * (1 / scale)), the reciprocal taken in fp32 on the host, one per-tensor scale for K
+// and one for V; a thread quantizes 16 elements into one 16-byte pool chunk.
 #include <type_traits>
 
 #include "common.h"
 
 namespace mllm {
 namespace {
+
+template <typename T>
+__device__ __forceinline__ float to_f32(uint16_t b) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return bf16_bits_to_f32(b);
+  else
+    return f16_bits_to_f32(b);
+}
+template <typename T>
+__device__ __forceinline__ uint16_t from_f32(float f) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return f32_to_bf16_bits(f);
+  else
+    return f32_to_f16_bits(f);
+}
+
+// Four 16-bit values (two dwords) -> four e4m3fn bytes of x * inv.
+template <typename T>
+__device__ __forceinline__ uint32_t quant4(uint32_t w0, uint32_t w1, float inv) {
+  return f32_to_e4m3fn_bits(to_f32<T>((uint16_t)w0) * inv) |
+         (f32_to_e4m3fn_bits(to_f32<T>((uint16_t)(w0 >> 16)) * inv) << 8) |
+         (f32_to_e4m3fn_bits(to_f32<T>((uint16_t)w1) * inv) << 16) |
+         (f32_to_e4m3fn_bits(to_f32<T>((uint16_t)(w1 >> 16)) * inv) << 24);
+}
+// Eight 16-bit values (16 bytes) -> eight e4m3fn bytes.
+template <typename T>
+__device__ __forceinline__ u32x2 quant8(u32x4 x, float inv) {
+  return u32x2{quant4<T>(x[0], x[1], inv), quant4<T>(x[2], x[3], inv)};
+}
 
 __global__ __launch_bounds__(256) void kv_append_vec_kernel(const char* __restrict__ k, int64_t k_st, int64_t k_sh,
                                                            const char* __restrict__ v, int64_t v_st, int64_t v_sh,
@@ -31,6 +64,31 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(const char* __restri
   const char* src = is_v ? v + t * v_st + h * v_sh : k + t * k_st + h * k_sh;
   char* dst = (is_v ? v_cache : k_cache) + (slot * per_tok + rem) * 16;
   st16(dst, ld16(src + (int64_t)ch * 16));
+}
+
+// fp8 pool: one thread per 16 elements of a (token, head) row: 32 source bytes -> one 16-byte chunk.
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_fp8_kernel(const char* __restrict__ k, int64_t k_st, int64_t k_sh,
+                                                           const char* __restrict__ v, int64_t v_st, int64_t v_sh,
+                                                           char* __restrict__ k_cache, char* __restrict__ v_cache,
+                                                           int64_t num_slots, int32_t hkv, int32_t chunks_per_head,
+                                                           const int64_t* __restrict__ slots, int64_t num_tokens,
+                                                           float k_inv, float v_inv) {
+  // source strides in bytes
+  const int64_t per_tok = (int64_t)hkv * chunks_per_head;
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= num_tokens * per_tok) return;
+  const int64_t t = c / per_tok;
+  const int64_t rem = c - t * per_tok;
+  const int h = (int)(rem / chunks_per_head);
+  const int ch = (int)(rem - (int64_t)h * chunks_per_head);
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const bool is_v = blockIdx.y != 0;
+  const char* src = (is_v ? v + t * v_st + h * v_sh : k + t * k_st + h * k_sh) + (int64_t)ch * 32;
+  const float inv = is_v ? v_inv : k_inv;
+  const u32x2 lo = quant8<T>(ld16(src), inv), hi = quant8<T>(ld16(src + 16), inv);
+  st16((is_v ? v_cache : k_cache) + (slot * per_tok + rem) * 16, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
 
 template <int SRC, int DST>
@@ -142,6 +200,44 @@ extern "C" int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_str
   return fail(MLLM_ERR_UNSUPPORTED, "mllm_kv_append: dtype pair");
 }
 
+extern "C" int mllm_kv_append_fp8(const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                                  int64_t v_stride_tok, int64_t v_stride_head, int32_t src_dtype, void* k_cache,
+                                  void* v_cache, int64_t num_slots, int32_t num_kv_heads, int32_t head_dim,
+                                  const int64_t* slot_mapping, int64_t num_tokens, float k_scale, float v_scale,
+                                  void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(src_dtype == MLLM_DTYPE_BF16 || src_dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
+               "mllm_kv_append_fp8: k and v must be bfloat16 or float16");
+  MLLM_REQUIRE(num_tokens >= 0 && num_slots >= 0 && num_kv_heads > 0 && head_dim > 0, MLLM_ERR_INVALID,
+               "mllm_kv_append_fp8: bad sizes");
+  MLLM_REQUIRE(head_dim % 16 == 0, MLLM_ERR_UNSUPPORTED, "mllm_kv_append_fp8: head_dim must be a multiple of 16");
+  MLLM_REQUIRE(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY, MLLM_ERR_INVALID,
+               "mllm_kv_append_fp8: scales must be positive and finite");
+  if (num_tokens == 0) return MLLM_OK;
+  MLLM_REQUIRE(k && v && k_cache && v_cache && slot_mapping, MLLM_ERR_INVALID, "mllm_kv_append_fp8: null pointer");
+  const bool aligned = ((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0 &&
+                       (k_stride_tok * 2) % 16 == 0 && (k_stride_head * 2) % 16 == 0 &&
+                       (v_stride_tok * 2) % 16 == 0 && (v_stride_head * 2) % 16 == 0;
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_kv_append_fp8: rows must be 16-byte aligned");
+  const int cph = head_dim / 16;
+  const int64_t total = num_tokens * num_kv_heads * cph;
+  MLLM_REQUIRE(total < (1ll << 40), MLLM_ERR_UNSUPPORTED, "mllm_kv_append_fp8: too many tokens");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)((total + 255) / 256), 2);
+  const float k_inv = 1.f / k_scale, v_inv = 1.f / v_scale;
+  if (src_dtype == MLLM_DTYPE_BF16)
+    kv_append_fp8_kernel<BF16><<<grid, 256, 0, st>>>((const char*)k, k_stride_tok * 2, k_stride_head * 2,
+                                                     (const char*)v, v_stride_tok * 2, v_stride_head * 2,
+                                                     (char*)k_cache, (char*)v_cache, num_slots, num_kv_heads, cph,
+                                                     slot_mapping, num_tokens, k_inv, v_inv);
+  else
+    kv_append_fp8_kernel<F16><<<grid, 256, 0, st>>>((const char*)k, k_stride_tok * 2, k_stride_head * 2,
+                                                    (const char*)v, v_stride_tok * 2, v_stride_head * 2,
+                                                    (char*)k_cache, (char*)v_cache, num_slots, num_kv_heads, cph,
+                                                    slot_mapping, num_tokens, k_inv, v_inv);
+  return check_launch("mllm_kv_append_fp8");
+}
+
 // ---------------------------------------------------------------- rotary embedding fused with the append
 // out[d] = x[d] * cos[d] + rotate_half(x)[d] * sin[d], rotate_half(x) = cat(-x[half:], x[:half])
 // (reference src/minillm/model/llama.py:58-72), evaluated the way torch evaluates that expression on
@@ -153,20 +249,6 @@ extern "C" int mllm_kv_append(const void* k, int64_t k_stride_tok, int64_t k_str
 namespace mllm {
 namespace {
 
-template <typename T>
-__device__ __forceinline__ float to_f32(uint16_t b) {
-  if constexpr (std::is_same<T, BF16>::value)
-    return bf16_bits_to_f32(b);
-  else
-    return f16_bits_to_f32(b);
-}
-template <typename T>
-__device__ __forceinline__ uint16_t from_f32(float f) {
-  if constexpr (std::is_same<T, BF16>::value)
-    return f32_to_bf16_bits(f);
-  else
-    return f32_to_f16_bits(f);
-}
 // round(round(x c) + round(r s)) in the 16-bit type.  The rounded products pass through an empty asm:
 // for fp16 the compiler narrows these float ops to native half arithmetic and would otherwise fuse the
 // first product into the sum's fma, skipping that product's own rounding.
@@ -183,13 +265,16 @@ union Chunk {
   uint16_t e[8];
 };
 
-template <typename T>
+// Q8: the pool is e4m3fn: the rotated k (rounded to T, as the unfused sequence stores it before the
+// append) and v are quantized with k_inv / v_inv, 8 bytes per half row instead of 16.
+template <typename T, bool Q8>
 __global__ __launch_bounds__(256) void rope_append_kernel(
     const char* __restrict__ q, int64_t q_st, int64_t q_sh, const char* __restrict__ k, int64_t k_st, int64_t k_sh,
     const char* __restrict__ v, int64_t v_st, int64_t v_sh, const char* __restrict__ cosp,
     const char* __restrict__ sinp, int64_t cs_st, char* __restrict__ q_out, int64_t qo_st, int64_t qo_sh,
     char* __restrict__ k_cache, char* __restrict__ v_cache, int64_t num_slots, int32_t H, int32_t Hkv,
-    int32_t half_bytes, int32_t chunks, const int64_t* __restrict__ slots, int64_t num_tokens) {
+    int32_t half_bytes, int32_t chunks, const int64_t* __restrict__ slots, int64_t num_tokens, float k_inv,
+    float v_inv) {
   // strides in bytes; one thread = one 16-byte chunk of the first half and its partner in the second
   const int rows = H + 2 * Hkv;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -199,9 +284,11 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
   const int row = rem / chunks;
   const int64_t lo = (int64_t)(rem - row * chunks) * 16;  // byte offset of the chunk in the first half
   const int64_t row_bytes = 2 * (int64_t)half_bytes;
+  const int64_t pool_row = Q8 ? row_bytes / 2 : row_bytes;  // bytes of one (slot, head) row of the pool
   const char* src;
   char* dst;
-  bool rotate = true;
+  bool rotate = true, to_pool = false;
+  float inv = 1.f;
   if (row < H) {
     src = q + t * q_st + row * q_sh;
     dst = q_out + t * qo_st + row * qo_sh;
@@ -209,13 +296,16 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     const int64_t slot = slots[t];
     if (slot < 0 || slot >= num_slots) return;
     const int kh = row - H;
+    to_pool = true;
     if (kh < Hkv) {
       src = k + t * k_st + kh * k_sh;
-      dst = k_cache + (slot * Hkv + kh) * row_bytes;
+      dst = k_cache + (slot * Hkv + kh) * pool_row;
+      inv = k_inv;
     } else {
       src = v + t * v_st + (kh - Hkv) * v_sh;
-      dst = v_cache + (slot * Hkv + kh - Hkv) * row_bytes;
+      dst = v_cache + (slot * Hkv + kh - Hkv) * pool_row;
       rotate = false;
+      inv = v_inv;
     }
   }
   Chunk x1, x2;
@@ -237,12 +327,73 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     x1 = o1;
     x2 = o2;
   }
+  if (Q8 && to_pool) {
+    st8(dst + lo / 2, quant8<T>(x1.v, inv));
+    st8(dst + half_bytes / 2 + lo / 2, quant8<T>(x2.v, inv));
+    return;
+  }
   st16(dst + lo, x1.v);
   st16(dst + half_bytes + lo, x2.v);
 }
 
 }  // namespace
 }  // namespace mllm
+
+namespace {
+
+int rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k, int64_t k_stride_tok,
+                   int64_t k_stride_head, const void* v, int64_t v_stride_tok, int64_t v_stride_head, const void* cos,
+                   const void* sin, int64_t cs_stride_tok, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t dtype, void* q_out, int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_cache,
+                   void* v_cache, int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens, bool fp8,
+                   float k_scale, float v_scale, void* stream) {
+  using namespace mllm;
+  const std::string fn = fp8 ? "mllm_rope_kv_append_fp8" : "mllm_rope_kv_append";
+  MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
+               fn + ": dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(num_tokens >= 0 && num_slots >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0,
+               MLLM_ERR_INVALID, fn + ": bad sizes");
+  MLLM_REQUIRE(head_dim % 16 == 0, MLLM_ERR_UNSUPPORTED, fn + ": head_dim must be a multiple of 16");
+  MLLM_REQUIRE(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY, MLLM_ERR_INVALID,
+               fn + ": scales must be positive and finite");
+  if (num_tokens == 0) return MLLM_OK;
+  MLLM_REQUIRE(q && k && v && cos && sin && q_out && k_cache && v_cache && slot_mapping, MLLM_ERR_INVALID,
+               fn + ": null pointer");
+  const int64_t strides[] = {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok,
+                             v_stride_head, cs_stride_tok, q_out_stride_tok, q_out_stride_head};
+  bool aligned = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)q_out |
+                  (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
+  for (int64_t s : strides) aligned = aligned && (s * 2) % 16 == 0;
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, fn + ": rows must be 16-byte aligned");
+  const int chunks = head_dim / 16;  // 16-byte chunks per half row
+  const int64_t total = num_tokens * (num_heads + 2 * num_kv_heads) * chunks;
+  MLLM_REQUIRE(total < (1ll << 40), MLLM_ERR_UNSUPPORTED, fn + ": too many tokens");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  const float k_inv = 1.f / k_scale, v_inv = 1.f / v_scale;
+  auto launch = [&](auto tag, auto q8) {
+    using T = decltype(tag);
+    rope_append_kernel<T, decltype(q8)::value><<<grid, 256, 0, st>>>(
+        (const char*)q, q_stride_tok * 2, q_stride_head * 2, (const char*)k, k_stride_tok * 2, k_stride_head * 2,
+        (const char*)v, v_stride_tok * 2, v_stride_head * 2, (const char*)cos, (const char*)sin, cs_stride_tok * 2,
+        (char*)q_out, q_out_stride_tok * 2, q_out_stride_head * 2, (char*)k_cache, (char*)v_cache, num_slots,
+        num_heads, num_kv_heads, head_dim, chunks, slot_mapping, num_tokens, k_inv, v_inv);
+  };
+  if (dtype == MLLM_DTYPE_BF16) {
+    if (fp8)
+      launch(BF16{}, std::true_type{});
+    else
+      launch(BF16{}, std::false_type{});
+  } else {
+    if (fp8)
+      launch(F16{}, std::true_type{});
+    else
+      launch(F16{}, std::false_type{});
+  }
+  return check_launch(fn.c_str());
+}
+
+}  // namespace
 
 extern "C" int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
                                    int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
@@ -251,37 +402,22 @@ extern "C" int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t 
                                    void* q_out, int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_cache,
                                    void* v_cache, int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens,
                                    void* stream) {
-  using namespace mllm;
-  MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
-               "mllm_rope_kv_append: dtype must be bfloat16 or float16");
-  MLLM_REQUIRE(num_tokens >= 0 && num_slots >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0,
-               MLLM_ERR_INVALID, "mllm_rope_kv_append: bad sizes");
-  MLLM_REQUIRE(head_dim % 16 == 0, MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: head_dim must be a multiple of 16");
-  if (num_tokens == 0) return MLLM_OK;
-  MLLM_REQUIRE(q && k && v && cos && sin && q_out && k_cache && v_cache && slot_mapping, MLLM_ERR_INVALID,
-               "mllm_rope_kv_append: null pointer");
-  const int64_t strides[] = {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok,
-                             v_stride_head, cs_stride_tok, q_out_stride_tok, q_out_stride_head};
-  bool aligned = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)q_out |
-                  (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
-  for (int64_t s : strides) aligned = aligned && (s * 2) % 16 == 0;
-  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: rows must be 16-byte aligned");
-  const int chunks = head_dim / 16;  // 16-byte chunks per half row
-  const int64_t total = num_tokens * (num_heads + 2 * num_kv_heads) * chunks;
-  MLLM_REQUIRE(total < (1ll << 40), MLLM_ERR_UNSUPPORTED, "mllm_rope_kv_append: too many tokens");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const unsigned grid = (unsigned)((total + 255) / 256);
-  auto launch = [&](auto tag) {
-    using T = decltype(tag);
-    rope_append_kernel<T><<<grid, 256, 0, st>>>(
-        (const char*)q, q_stride_tok * 2, q_stride_head * 2, (const char*)k, k_stride_tok * 2, k_stride_head * 2,
-        (const char*)v, v_stride_tok * 2, v_stride_head * 2, (const char*)cos, (const char*)sin, cs_stride_tok * 2,
-        (char*)q_out, q_out_stride_tok * 2, q_out_stride_head * 2, (char*)k_cache, (char*)v_cache, num_slots,
-        num_heads, num_kv_heads, head_dim, chunks, slot_mapping, num_tokens);
-  };
-  if (dtype == MLLM_DTYPE_BF16)
-    launch(BF16{});
-  else
-    launch(F16{});
-  return check_launch("mllm_rope_kv_append");
+  return rope_kv_append(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v, v_stride_tok,
+                        v_stride_head, cos, sin, cs_stride_tok, num_heads, num_kv_heads, head_dim, dtype, q_out,
+                        q_out_stride_tok, q_out_stride_head, k_cache, v_cache, num_slots, slot_mapping, num_tokens,
+                        false, 1.f, 1.f, stream);
+}
+
+extern "C" int mllm_rope_kv_append_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+                                       int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                                       int64_t v_stride_tok, int64_t v_stride_head, const void* cos, const void* sin,
+                                       int64_t cs_stride_tok, int32_t num_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t dtype, void* q_out, int64_t q_out_stride_tok,
+                                       int64_t q_out_stride_head, void* k_cache, void* v_cache, int64_t num_slots,
+                                       const int64_t* slot_mapping, int64_t num_tokens, float k_scale, float v_scale,
+                                       void* stream) {
+  return rope_kv_append(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v, v_stride_tok,
+                        v_stride_head, cos, sin, cs_stride_tok, num_heads, num_kv_heads, head_dim, dtype, q_out,
+                        q_out_stride_tok, q_out_stride_head, k_cache, v_cache, num_slots, slot_mapping, num_tokens,
+                        true, k_scale, v_scale, stream);
 }

@@ -26,6 +26,12 @@
 // 0 and pool slots past a row's length are never read).  The grid is 1-D with the KV head fastest,
 // so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and
 // keeps that head's shared-prefix pages in its own L2.
+//
+// fp8 (e4m3fn) pools: the DMA cannot widen, so tiles go through VGPRs instead.  At the even phase where
+// the 16-bit kernel issues its DMA, each lane loads 16 pool bytes of its wavefront's 8 tile rows; at
+// the end of the next (odd) phase it widens them to bf16/fp16 (exact) and writes them with ds_write_b128
+// into the same swizzled LDS layout, before the barrier that publishes them.  Everything downstream of
+// LDS is the 16-bit kernel; k_scale is folded into the softmax scale and v_scale into the output.
 #include <math.h>
 
 #include "common.h"
@@ -59,7 +65,8 @@ struct PrefillArgs {
   const int32_t* seq_lens;
   const int2* work;
   int QT;
-  float scale_log2;
+  float scale_log2;  // softmax scale x k_scale x log2(e)
+  float v_scale;     // output scale of an fp8 pool
   uint16_t* out;
   int64_t o_st, o_sh;
 };
@@ -121,6 +128,29 @@ __device__ __forceinline__ void dma_tile(const char* pool, const PrefillArgs& a,
       dma16(base, slot_bytes + head_bytes + 16u * c, dst + 4 * i * kRowBytes);
     }
   }
+}
+
+// fp8 pools: this wavefront's share of a tile (rows 8 w .. 8 w + 7, 128 bytes each) is one 16-byte load
+// per lane: row 8 w + l / 8, dims 16 (l % 8) .. +15.  off: the lane's offset from the group base for a
+// full tile.  Keys past `last` load the row of `last`, as in dma_tile.
+__device__ __forceinline__ u32x4 stage_load(const char* pool, const PrefillArgs& a, int blk, int kv0, int last,
+                                            int kv_end, int w, unsigned off, unsigned head_bytes, int lane) {
+  if (kv0 + kBN <= kv_end) return ld16(group_base(pool, a, blk, kv0 + 16 * (w >> 1)) + off);
+  const int r = 8 * w + (lane >> 3);
+  const unsigned slot_bytes = (unsigned)(min(kv0 + r, last) & (a.bs - 1)) * (unsigned)a.row_bytes;
+  return ld16(group_base(pool, a, blk, 0) + (slot_bytes + head_bytes + 16u * (lane & 7)));
+}
+
+// Widens a lane's 16 fp8 values to two 16-byte chunks of 16-bit values (logical chunks 2 (l % 8) and
+// 2 (l % 8) + 1 of row 8 w + l / 8) and writes them at their swizzled places in the LDS tile.
+template <typename T, bool IS_V>
+__device__ __forceinline__ void stage_store(u32x4 x, int w, int lane, char* slot) {
+  const int r = 8 * w + (lane >> 3);
+  const int c0 = 2 * (lane & 7);
+  const int sw = IS_V ? 4 * (r & 3) : (r & 15);
+  char* row = slot + r * kRowBytes;
+  *reinterpret_cast<u32x4*>(row + 16 * (c0 ^ sw)) = fp8x8_to<T>(x[0], x[1]);
+  *reinterpret_cast<u32x4*>(row + 16 * ((c0 + 1) ^ sw)) = fp8x8_to<T>(x[2], x[3]);
 }
 
 // Workgroup barrier that first waits for this wavefront's LDS reads and for all but its N most recent
@@ -297,7 +327,7 @@ __device__ __forceinline__ void matrix_phase(const char* lds, unsigned vb, unsig
 // K(s+3) (into the slot of K(s-1)), both freed by the barrier that ended phase 2s-1; the barrier that
 // ends phase 2s+1 waits for everything but those, so the tiles phase 2s+2 reads (K(s+2), V(s+1)) have
 // landed in every wavefront's share.
-template <typename T>
+template <typename T, bool F8>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   const int tid = threadIdx.x;
@@ -330,13 +360,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const float c = a.scale_log2;
 
   // load lanes: tile rows r0, r1 of this wavefront's two DMA instructions; offsets from the group base
-  const unsigned head_bytes = (unsigned)(kvh * kRowBytes);
+  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * (F8 ? 1 : 2));
   const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
   const unsigned rb = (unsigned)a.row_bytes;
   const unsigned koff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * k_chunk(r0, lane);
   const unsigned koff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * k_chunk(r1, lane);
   const unsigned voff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * v_chunk(r0, lane);
   const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
+  const unsigned soff = (unsigned)(8 * (wave & 1) + (lane >> 3)) * rb + head_bytes + 16u * (lane & 7);  // fp8
   // operand reads (see scores / pv_tile)
   const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
   const unsigned vread = (unsigned)(kVBase + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
@@ -382,20 +413,32 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
 
   // prologue: K(0), V(0), K(1), V(1), K(2); K(0), V(0) and K(1) have landed after the first barrier
-  {
-    const int b0 = blk_of(0);
-    dma_tile<false>(kc, a, b0, 0, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(0));
-    dma_tile<true>(vc, a, b0, 0, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(0));
+  if constexpr (F8) {
+    for (int t = 0; t < min(ntiles, 3); ++t) {
+      const int b = blk_of(t);
+      const u32x4 kx = stage_load(kc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
+      if (t < 2) {
+        const u32x4 vx = stage_load(vc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
+        stage_store<T, true>(vx, wu, lane, v_slot(t));
+      }
+      stage_store<T, false>(kx, wu, lane, k_slot(t));
+    }
+    barrier_vm<0>();
+  } else {
+    {
+      const int b0 = blk_of(0);
+      dma_tile<false>(kc, a, b0, 0, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(0));
+      dma_tile<true>(vc, a, b0, 0, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(0));
+    }
+    if (ntiles > 1) {
+      const int b1 = blk_of(1);
+      dma_tile<false>(kc, a, b1, kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(1));
+      dma_tile<true>(vc, a, b1, kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(1));
+    }
+    if (ntiles > 2)
+      dma_tile<false>(kc, a, blk_of(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(2));
+    barrier_vm_n(2 * (ntiles > 1) + 2 * (ntiles > 2));
   }
-  if (ntiles > 1) {
-    const int b1 = blk_of(1);
-    dma_tile<false>(kc, a, b1, kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(1));
-    dma_tile<true>(vc, a, b1, kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(1));
-  }
-  if (ntiles > 2)
-    dma_tile<false>(kc, a, blk_of(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes,
-                    lane, k_slot(2));
-  barrier_vm_n(2 * (ntiles > 1) + 2 * (ntiles > 2));
 
   STile st;
   u32x4 pf[2][2];
@@ -405,6 +448,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   }
 
   int issued = 0;  // DMA instructions of the last even phase
+  u32x4 kst = {0, 0, 0, 0}, vst = {0, 0, 0, 0};  // fp8: K(s+3), V(s+2) between their load and LDS store
   for (int p = 0; p < 2 * ntiles; ++p) {
     const int s = p >> 1;
     if ((p & 1) == 0) {
@@ -416,11 +460,17 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       }
       issued = 0;
       if (s + 2 < ntiles) {
-        dma_tile<true>(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(s + 2));
+        if constexpr (F8)
+          vst = stage_load(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, soff, head_bytes, lane);
+        else
+          dma_tile<true>(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(s + 2));
         issued += 2;
       }
       if (s + 3 < ntiles) {
-        dma_tile<false>(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(s + 3));
+        if constexpr (F8)
+          kst = stage_load(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, soff, head_bytes, lane);
+        else
+          dma_tile<false>(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(s + 3));
         issued += 2;
       }
     }
@@ -439,14 +489,21 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       const int j = (p + 1) >> 1;
       if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
     }
-    if (p & 1)
-      barrier_vm_n(issued);
-    else
+    if (p & 1) {
+      if constexpr (F8) {  // the slots of V(s-1) and K(s-1) are free since the barrier that ended phase 2s-1
+        if (s + 2 < ntiles) stage_store<T, true>(vst, wu, lane, v_slot(s + 2));
+        if (s + 3 < ntiles) stage_store<T, false>(kst, wu, lane, k_slot(s + 3));
+        barrier_vm<0>();
+      } else {
+        barrier_vm_n(issued);
+      }
+    } else {
       barrier_lds();
+    }
   }
 
   if (!row_valid) return;
-  const float inv = 1.f / l_run;
+  const float inv = (F8 ? a.v_scale : 1.f) / l_run;
   const int head = kvh * a.G + (n % a.G);
   uint16_t* orow = a.out + (int64_t)(qs + tok) * a.o_st + (int64_t)head * a.o_sh;
   // oacc[dt][r]: dim 32 dt + 8 (r / 4) + 4 h + r % 4
@@ -464,37 +521,42 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 }  // namespace
 }  // namespace mllm
 
-extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+namespace {
+
+int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                                   const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
                                   int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
                                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
                                   const int32_t* prefill_work, int32_t num_prefill_work, int32_t q_tile_tokens,
                                   float softmax_scale, int32_t dtype, void* out, int64_t out_stride_tok,
-                                  int64_t out_stride_head, void* stream) {
+                                  int64_t out_stride_head, bool fp8, float k_scale, float v_scale, void* stream) {
   using namespace mllm;
+  const std::string fn = fp8 ? "mllm_paged_prefill_fp8" : "mllm_paged_prefill";
   MLLM_REQUIRE(dtype == MLLM_DTYPE_BF16 || dtype == MLLM_DTYPE_F16, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_prefill: dtype must be bfloat16 or float16");
-  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: head_dim must be 128");
+               fn + ": dtype must be bfloat16 or float16");
+  MLLM_REQUIRE(head_dim == kHeadDim, MLLM_ERR_UNSUPPORTED, fn + ": head_dim must be 128");
+  MLLM_REQUIRE(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY, MLLM_ERR_INVALID,
+               fn + ": scales must be positive and finite");
   MLLM_REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0, MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_prefill: block_size must be a power of two >= 16");
+               fn + ": block_size must be a power of two >= 16");
   MLLM_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, MLLM_ERR_INVALID,
-               "mllm_paged_prefill: num_heads must be a multiple of num_kv_heads");
+               fn + ": num_heads must be a multiple of num_kv_heads");
   const int G = num_heads / num_kv_heads;
-  MLLM_REQUIRE(32 % G == 0, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: H / Hkv must divide 32");
+  MLLM_REQUIRE(32 % G == 0, MLLM_ERR_UNSUPPORTED, fn + ": H / Hkv must divide 32");
   MLLM_REQUIRE(q_tile_tokens == kQTileRows / G, MLLM_ERR_INVALID,
-               "mllm_paged_prefill: q_tile_tokens must be 256 / (H / Hkv)");
-  MLLM_REQUIRE(num_prefill_work >= 0, MLLM_ERR_INVALID, "mllm_paged_prefill: negative count");
+               fn + ": q_tile_tokens must be 256 / (H / Hkv)");
+  MLLM_REQUIRE(num_prefill_work >= 0, MLLM_ERR_INVALID, fn + ": negative count");
   if (num_prefill_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && prefill_work,
-               MLLM_ERR_INVALID, "mllm_paged_prefill: null pointer");
+               MLLM_ERR_INVALID, fn + ": null pointer");
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)out % 8 == 0) && ((uintptr_t)k_cache % 16 == 0) &&
                        ((uintptr_t)v_cache % 16 == 0) && (q_stride_tok * 2) % 16 == 0 &&
                        (q_stride_head * 2) % 16 == 0 && (out_stride_tok * 2) % 8 == 0 && (out_stride_head * 2) % 8 == 0;
-  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: q, out and pools need aligned rows");
+  MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, fn + ": q, out and pools need aligned rows");
   MLLM_REQUIRE((int64_t)num_prefill_work * num_kv_heads < (1ll << 31), MLLM_ERR_UNSUPPORTED,
-               "mllm_paged_prefill: too many work items");
+               fn + ": too many work items");
   MLLM_REQUIRE(num_kv_heads * head_dim * 2 < (1 << 24) && (int64_t)block_size * num_kv_heads * head_dim * 2 < (1ll << 32),
-               MLLM_ERR_UNSUPPORTED, "mllm_paged_prefill: KV block too large");
+               MLLM_ERR_UNSUPPORTED, fn + ": KV block too large");
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_tok;
@@ -502,7 +564,7 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   a.kc = static_cast<const uint16_t*>(k_cache);
   a.vc = static_cast<const uint16_t*>(v_cache);
   a.num_blocks = num_blocks;
-  a.row_bytes = num_kv_heads * head_dim * 2;
+  a.row_bytes = num_kv_heads * head_dim * (fp8 ? 1 : 2);
   a.page_bytes = (unsigned)((int64_t)block_size * a.row_bytes);
   a.bs = block_size;
   a.bs_shift = __builtin_ctz((unsigned)block_size);
@@ -515,15 +577,51 @@ extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q
   a.seq_lens = seq_lens;
   a.work = reinterpret_cast<const int2*>(prefill_work);
   a.QT = q_tile_tokens;
-  a.scale_log2 = softmax_scale * kLog2e;
+  a.scale_log2 = softmax_scale * k_scale * kLog2e;
+  a.v_scale = v_scale;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
-  if (dtype == MLLM_DTYPE_BF16)
-    prefill_kernel<BF16><<<grid, 512, 0, st>>>(a);
-  else
-    prefill_kernel<F16><<<grid, 512, 0, st>>>(a);
-  return check_launch("mllm_paged_prefill");
+  if (dtype == MLLM_DTYPE_BF16) {
+    if (fp8)
+      prefill_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
+    else
+      prefill_kernel<BF16, false><<<grid, 512, 0, st>>>(a);
+  } else {
+    if (fp8)
+      prefill_kernel<F16, true><<<grid, 512, 0, st>>>(a);
+    else
+      prefill_kernel<F16, false><<<grid, 512, 0, st>>>(a);
+  }
+  return check_launch(fn.c_str());
+}
+
+}  // namespace
+
+extern "C" int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                  const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                  const int32_t* prefill_work, int32_t num_prefill_work, int32_t q_tile_tokens,
+                                  float softmax_scale, int32_t dtype, void* out, int64_t out_stride_tok,
+                                  int64_t out_stride_head, void* stream) {
+  return paged_prefill(q, q_stride_tok, q_stride_head, k_cache, v_cache, num_blocks, block_size, num_heads,
+                       num_kv_heads, head_dim, qo_indptr, kv_indptr, kv_indices, seq_lens, prefill_work,
+                       num_prefill_work, q_tile_tokens, softmax_scale, dtype, out, out_stride_tok, out_stride_head,
+                       false, 1.f, 1.f, stream);
+}
+
+extern "C" int mllm_paged_prefill_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                      const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                                      const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                      const int32_t* prefill_work, int32_t num_prefill_work, int32_t q_tile_tokens,
+                                      float softmax_scale, int32_t dtype, float k_scale, float v_scale, void* out,
+                                      int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  return paged_prefill(q, q_stride_tok, q_stride_head, k_cache, v_cache, num_blocks, block_size, num_heads,
+                       num_kv_heads, head_dim, qo_indptr, kv_indptr, kv_indices, seq_lens, prefill_work,
+                       num_prefill_work, q_tile_tokens, softmax_scale, dtype, out, out_stride_tok, out_stride_head,
+                       true, k_scale, v_scale, stream);
 }

@@ -43,6 +43,17 @@ SIGNATURES = {
     "mllm_dense_attention": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
                                             _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i64, _i64,
                                             _p]),
+    # fp8 (e4m3fn) pools with per-tensor k_scale / v_scale
+    "mllm_kv_append_fp8": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _i64, _i32, _i32, _p, _i64, _f32,
+                                          _f32, _p]),
+    "mllm_rope_kv_append_fp8": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32,
+                                               _i32, _i32, _i32, _p, _i64, _i64, _p, _p, _i64, _p, _i64, _f32, _f32,
+                                               _p]),
+    "mllm_paged_decode_fp8": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
+                                             _i32, _p, _i32, _i32, _f32, _i32, _f32, _f32, _p, _i64, _i64, _p, _i64,
+                                             _p]),
+    "mllm_paged_prefill_fp8": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
+                                              _i32, _i32, _f32, _i32, _f32, _f32, _p, _i64, _i64, _p]),
 }
 
 

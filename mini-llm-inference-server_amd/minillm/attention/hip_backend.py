@@ -11,6 +11,11 @@ Per layer, `forward` issues on the current stream:
 A work plan (`mllm_plan`) is built on the GPU the first time a given `meta` is seen and reused by the
 other layers, like FlashInfer's plan()/run() split (flashinfer_backend.py:44).  Nothing synchronises
 the host, and there is no fallback: a missing library raises RuntimeError at construction.
+
+A pool of dtype torch.float8_e4m3fn (the reference's planned fp8 KV cache, M9b in
+docs/distributed_inference_plan.md:310) selects the `_fp8` entry points: the append stores
+e4m3fn(x * (1 / scale)) and attention reads value * scale, with per-tensor `k_scale` / `v_scale` passed
+to `forward`; q, k, v and the output stay bf16 / fp16.
 """
 
 from __future__ import annotations
@@ -56,6 +61,13 @@ def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None or t.numel() == 0 else t.data_ptr()
 
 
+FP8 = torch.float8_e4m3fn
+
+
+def is_fp8(pool: torch.Tensor) -> bool:
+    return pool.dtype == FP8
+
+
 class HipBackend(AttentionBackend):
     name = "hip"
     # The model hands q and k to `forward_rotary` before RoPE when this is set (LlamaAttention checks it),
@@ -70,14 +82,14 @@ class HipBackend(AttentionBackend):
 
     # ------------------------------------------------------------------ paged path
 
-    def forward(self, q, k, v, k_cache, v_cache, meta):
-        q, k, v = self._check(q, k, v, k_cache, v_cache, meta)
-        self.append(k, v, k_cache, v_cache, meta)
+    def forward(self, q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
+        q, k, v = self._check(q, k, v, k_cache, v_cache, meta, k_scale, v_scale)
+        self.append(k, v, k_cache, v_cache, meta, k_scale, v_scale)
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        self.attend(q, k_cache, v_cache, meta, out)
+        self.attend(q, k_cache, v_cache, meta, out, k_scale, v_scale)
         return out
 
-    def _check(self, q, k, v, k_cache, v_cache, meta):
+    def _check(self, q, k, v, k_cache, v_cache, meta, k_scale=1.0, v_scale=1.0):
         n, h, dh = q.shape
         if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
             raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, Hkv, Dh]")
@@ -90,44 +102,63 @@ class HipBackend(AttentionBackend):
             raise ValueError("num_heads must be a multiple of num_kv_heads")
         if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
             raise ValueError("the KV pools must be contiguous")
-        if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
-            raise ValueError("q and the pools must share one dtype")
+        if v_cache.dtype != k_cache.dtype:
+            raise ValueError("k_cache and v_cache must share one dtype")
+        if is_fp8(k_cache):
+            if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+                raise ValueError("with an fp8 pool, q, k and v must share one dtype, bfloat16 or float16")
+            if not (0 < k_scale < math.inf and 0 < v_scale < math.inf):
+                raise ValueError("k_scale and v_scale must be positive and finite")
+        else:
+            if q.dtype != k_cache.dtype:
+                raise ValueError("q and the pools must share one dtype")
+            if k_scale != 1.0 or v_scale != 1.0:
+                raise ValueError("k_scale / v_scale apply to fp8 pools only")
         if n != meta.query_start_loc[-1]:
             raise ValueError(f"q has {n} tokens, the metadata describes {meta.query_start_loc[-1]}")
         return tuple(t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
 
-    def forward_rotary(self, q, k, v, cos, sin, k_cache, v_cache, meta):
+    def forward_rotary(self, q, k, v, cos, sin, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
         """`forward` with the model's RoPE folded in: q and k arrive before the rotation (reference
         src/minillm/model/llama.py:110 applies it right before the backend call), with the step's
         cos / sin rows [N, Dh].  One launch rotates q and k, appends the rotated k and v to the pool and
         writes the rotated q, bit for bit what apply_rotary followed by `forward` produces."""
-        q, k, v = self._check(q, k, v, k_cache, v_cache, meta)
-        q_rot = self.rope_append(q, k, v, cos, sin, k_cache, v_cache, meta)
+        q, k, v = self._check(q, k, v, k_cache, v_cache, meta, k_scale, v_scale)
+        q_rot = self.rope_append(q, k, v, cos, sin, k_cache, v_cache, meta, k_scale, v_scale)
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        self.attend(q_rot, k_cache, v_cache, meta, out)
+        self.attend(q_rot, k_cache, v_cache, meta, out, k_scale, v_scale)
         return out
 
-    def rope_append(self, q, k, v, cos, sin, k_cache, v_cache, meta):
+    def rope_append(self, q, k, v, cos, sin, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
         """Rotary embedding of q and k plus the KV append (`mllm_rope_kv_append`); returns the rotated q."""
         n, h, dh = q.shape
         num_blocks, bs, hkv, _ = k_cache.shape
         if cos.shape != (n, dh) or sin.shape != (n, dh):
             raise ValueError(f"cos and sin must be [N, Dh] = [{n}, {dh}]")
-        if cos.dtype != q.dtype or sin.dtype != q.dtype or k_cache.dtype != q.dtype:
-            raise ValueError("q, cos, sin and the pools must share one dtype")
+        if cos.dtype != q.dtype or sin.dtype != q.dtype or not (k_cache.dtype == q.dtype or is_fp8(k_cache)):
+            raise ValueError("q, cos, sin and the pools must share one dtype (or the pools be fp8)")
         if cos.stride(-1) != 1 or sin.stride() != cos.stride():
             cos, sin = cos.contiguous(), sin.contiguous()
         q_rot = torch.empty((n, h, dh), dtype=q.dtype, device=q.device)
-        self._lib.call("mllm_rope_kv_append", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
-                       k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos.data_ptr(), sin.data_ptr(),
-                       cos.stride(0), h, hkv, dh, _native.dtype_code(q.dtype), q_rot.data_ptr(), q_rot.stride(0),
-                       q_rot.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks * bs,
-                       meta.slot_mapping.data_ptr(), n, _native.stream_ptr(q.device))
+        args = (q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(),
+                v.stride(0), v.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0), h, hkv, dh,
+                _native.dtype_code(q.dtype), q_rot.data_ptr(), q_rot.stride(0), q_rot.stride(1), k_cache.data_ptr(),
+                v_cache.data_ptr(), num_blocks * bs, meta.slot_mapping.data_ptr(), n)
+        if is_fp8(k_cache):
+            self._lib.call("mllm_rope_kv_append_fp8", *args, k_scale, v_scale, _native.stream_ptr(q.device))
+        else:
+            self._lib.call("mllm_rope_kv_append", *args, _native.stream_ptr(q.device))
         return q_rot
 
-    def append(self, k, v, k_cache, v_cache, meta) -> None:
+    def append(self, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """KV append (reference write_kv, paged_torch_ref.py:23-28): one launch for K and V."""
         num_blocks, bs, hkv, dh = k_cache.shape
+        if is_fp8(k_cache):
+            self._lib.call("mllm_kv_append_fp8", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                           v.stride(1), _native.dtype_code(k.dtype), k_cache.data_ptr(), v_cache.data_ptr(),
+                           num_blocks * bs, hkv, dh, meta.slot_mapping.data_ptr(), k.shape[0], k_scale, v_scale,
+                           _native.stream_ptr(k_cache.device))
+            return
         self._lib.call("mllm_kv_append", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
                        v.stride(1), _native.dtype_code(k.dtype), k_cache.data_ptr(), v_cache.data_ptr(),
                        _native.dtype_code(k_cache.dtype), num_blocks * bs, hkv, dh, meta.slot_mapping.data_ptr(),
@@ -139,26 +170,30 @@ class HipBackend(AttentionBackend):
             self._make_plan(meta, num_heads, num_kv_heads, head_dim, device, _native.stream_ptr(device))
         return self._plan
 
-    def attend(self, q, k_cache, v_cache, meta, out) -> None:
+    def attend(self, q, k_cache, v_cache, meta, out, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """Attention of every new token over its row's context in the pool, written into `out`."""
         plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device)
         if plan.num_decode:
-            self.run_decode(q, k_cache, v_cache, meta, out)
+            self.run_decode(q, k_cache, v_cache, meta, out, k_scale, v_scale)
             self.run_merge(q, meta, out)
         if plan.num_prefill:
-            self.run_prefill(q, k_cache, v_cache, meta, out)
+            self.run_prefill(q, k_cache, v_cache, meta, out, k_scale, v_scale)
 
-    def run_decode(self, q, k_cache, v_cache, meta, out) -> None:
+    def run_decode(self, q, k_cache, v_cache, meta, out, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """Split-KV decode of the rows with one new token (reference paged_torch_ref.py:47-59)."""
         plan = self._plan
         num_blocks, bs, hkv, dh = k_cache.shape
         ws = self._workspace_for(plan.workspace_bytes, q.device)
-        self._lib.call("mllm_paged_decode", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
-                       v_cache.data_ptr(), num_blocks, bs, q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(),
-                       meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(), meta.seq_lens_i32.data_ptr(),
-                       _ptr(plan.decode_work), plan.num_decode, _ptr(plan.merge_work), plan.num_merge,
-                       plan.pages_per_split, dh ** -0.5, _native.dtype_code(k_cache.dtype), out.data_ptr(),
-                       out.stride(0), out.stride(1), _ptr(ws), plan.workspace_bytes, _native.stream_ptr(q.device))
+        args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, bs,
+                q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(),
+                meta.seq_lens_i32.data_ptr(), _ptr(plan.decode_work), plan.num_decode, _ptr(plan.merge_work),
+                plan.num_merge, plan.pages_per_split, dh ** -0.5, _native.dtype_code(q.dtype))
+        tail = (out.data_ptr(), out.stride(0), out.stride(1), _ptr(ws), plan.workspace_bytes,
+                _native.stream_ptr(q.device))
+        if is_fp8(k_cache):
+            self._lib.call("mllm_paged_decode_fp8", *args, k_scale, v_scale, *tail)
+        else:
+            self._lib.call("mllm_paged_decode", *args, *tail)
 
     def run_merge(self, q, meta, out) -> None:
         """Log-sum-exp merge of the decode rows that were split."""
@@ -170,16 +205,19 @@ class HipBackend(AttentionBackend):
                        out.stride(0), out.stride(1), _ptr(self._workspace), plan.workspace_bytes,
                        _native.stream_ptr(q.device))
 
-    def run_prefill(self, q, k_cache, v_cache, meta, out) -> None:
+    def run_prefill(self, q, k_cache, v_cache, meta, out, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """MFMA attention of the rows with several new tokens (reference paged_torch_ref.py:61-73)."""
         plan = self._plan
         num_blocks, bs, hkv, dh = k_cache.shape
-        self._lib.call("mllm_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
-                       v_cache.data_ptr(), num_blocks, bs, q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(),
-                       meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(), meta.seq_lens_i32.data_ptr(),
-                       _ptr(plan.prefill_work), plan.num_prefill, plan.q_tile, dh ** -0.5,
-                       _native.dtype_code(k_cache.dtype), out.data_ptr(), out.stride(0), out.stride(1),
-                       _native.stream_ptr(q.device))
+        args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, bs,
+                q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(),
+                meta.seq_lens_i32.data_ptr(), _ptr(plan.prefill_work), plan.num_prefill, plan.q_tile, dh ** -0.5,
+                _native.dtype_code(q.dtype))
+        tail = (out.data_ptr(), out.stride(0), out.stride(1), _native.stream_ptr(q.device))
+        if is_fp8(k_cache):
+            self._lib.call("mllm_paged_prefill_fp8", *args, k_scale, v_scale, *tail)
+        else:
+            self._lib.call("mllm_paged_prefill", *args, *tail)
 
     def _make_plan(self, meta, h: int, hkv: int, dh: int, dev, stream: int) -> None:
         news, lens, bs = meta.num_new, meta.seq_lens, meta.block_size

@@ -86,10 +86,13 @@ class EngineCore:
     def __init__(self, model, max_model_len: int | None = None, step_log: bool = False, max_batch_size: int = 1,
                  max_num_batched_tokens: int | None = None, num_kv_blocks: int | None = None,
                  enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None,
-                 chunked_prefill: bool = False) -> None:
+                 chunked_prefill: bool = False, kv_cache_dtype: torch.dtype | None = None,
+                 kv_scales: tuple[float, float] = (1.0, 1.0)) -> None:
         """`metadata_builder(seqs, block_size, device)` defaults to AttentionMetadata.build (the GPU
         build); a test may pass another implementation of the same contract.  `chunked_prefill` mixes
-        decode rows and prompt chunks in one step under the token budget (see Scheduler)."""
+        decode rows and prompt chunks in one step under the token budget (see Scheduler).
+        `kv_cache_dtype` defaults to the model's dtype; torch.float8_e4m3fn gives an fp8 pool whose K and
+        V tensors of every layer use the per-tensor scales `kv_scales` (k_scale, v_scale)."""
         self.model = model
         self.build_metadata = metadata_builder or AttentionMetadata.build
         p = next(model.parameters())
@@ -98,13 +101,17 @@ class EngineCore:
         self.max_batch_size = max_batch_size
         if num_kv_blocks is None:
             num_kv_blocks = max_batch_size * -(-self.max_model_len // BLOCK_SIZE)
-        self.cache = PagedKVCache(model.config, num_kv_blocks, self.device, self.dtype)
+        self.kv_dtype = kv_cache_dtype or self.dtype
+        self.cache = PagedKVCache(model.config, num_kv_blocks, self.device, self.kv_dtype, k_scale=kv_scales[0],
+                                  v_scale=kv_scales[1])
         self.prefix = PrefixCache() if enable_prefix_caching else None
         self.blocks = BlockManager(num_kv_blocks, BLOCK_SIZE, self.prefix)
         self.scheduler = Scheduler(max_batch_size, max_num_batched_tokens or DEFAULT_MAX_NUM_BATCHED_TOKENS,
                                    self.blocks, self.prefix, chunked_prefill=chunked_prefill)
-        self._salt_keys = {"block_size": BLOCK_SIZE, "kv_dtype": str(self.dtype).removeprefix("torch."),
+        self._salt_keys = {"block_size": BLOCK_SIZE, "kv_dtype": str(self.kv_dtype).removeprefix("torch."),
                            "layout": "NHD", "model": model_id}
+        if self.cache.quantized:  # the stored bytes depend on the scales too
+            self._salt_keys["kv_scales"] = [kv_scales[0], kv_scales[1]]
         self.step_log: list[StepRecord] | None = [] if step_log else None
         self._step = 0
         self._aborted: list[RequestOutput] = []

@@ -85,13 +85,15 @@ class LlamaAttention(nn.Module):
             # ragged step: one row of every sequence's new tokens -> [N, heads, Dh] views for the backend
             layer = self.layer_idx
             pools = (kv_cache.cache.k[layer], kv_cache.cache.v[layer], kv_cache.meta)
+            scales = kv_cache.cache.scales(layer)  # fp8 pools only
             if getattr(self.backend, "fuse_rotary", False) and b == 1:
                 # the backend rotates q and k itself, in the launch that appends k and v
                 out = self.backend.forward_rotary(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1),
-                                                  cos[0], sin[0], *pools)
+                                                  cos[0], sin[0], *pools, **scales)
             else:
                 q, k = apply_rotary(q, cos, sin), apply_rotary(k, cos, sin)
-                out = self.backend.forward(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), *pools)
+                out = self.backend.forward(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), *pools,
+                                           **scales)
             return self.o_proj(out.reshape(b, t, -1))
         q, k = apply_rotary(q, cos, sin), apply_rotary(k, cos, sin)
         if kv_cache is not None:

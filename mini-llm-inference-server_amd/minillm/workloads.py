@@ -51,22 +51,26 @@ class Workload:
     def lens(self) -> list[int]:
         return [c + n for c, n, _ in self.seqs]
 
-    def kv_bytes(self, rows=None) -> int:
-        """Context K+V bytes of the given rows (all rows by default)."""
+    def kv_bytes(self, rows=None, kv_elem: int = 2) -> int:
+        """Context K+V bytes of the given rows (all rows by default); kv_elem = pool bytes per element
+        (2 for bf16 / fp16, 1 for fp8)."""
         rows = range(len(self.seqs)) if rows is None else rows
-        return sum((self.seqs[i][0] + self.seqs[i][1]) * self.hkv * self.dh * 2 * 2 for i in rows)
+        return sum((self.seqs[i][0] + self.seqs[i][1]) * self.hkv * self.dh * kv_elem * 2 for i in rows)
 
-    def algorithmic_bytes(self) -> int:
+    def algorithmic_bytes(self, kv_elem: int = 2) -> int:
+        """Context K+V once, q in and o out (16-bit), the append's k/v read (16-bit) and pool write, page
+        ids and per-row indices."""
         n, s = self.num_tokens, len(self.seqs)
         pages = sum(-(-length // self.block_size) for length in self.lens)
-        return (self.kv_bytes() + n * self.h * self.dh * 2 * 2 + n * self.hkv * self.dh * 2 * 2 * 2 + 4 * pages
-                + 4 * (3 * s + 1))
+        return (self.kv_bytes(kv_elem=kv_elem) + n * self.h * self.dh * 2 * 2
+                + n * self.hkv * self.dh * 2 * (2 + kv_elem) + 4 * pages + 4 * (3 * s + 1))
 
-    def decode_kernel_bytes(self) -> int:
+    def decode_kernel_bytes(self, kv_elem: int = 2) -> int:
         """Algorithmic bytes of the decode launch alone: its rows' context K+V, their q and o, page ids."""
         rows = [i for i, (_, n, _) in enumerate(self.seqs) if n == 1]
         pages = sum(-(-self.lens[i] // self.block_size) for i in rows)
-        return self.kv_bytes(rows) + len(rows) * self.h * self.dh * 2 * 2 + 4 * pages + 4 * (3 * len(rows) + 1)
+        return (self.kv_bytes(rows, kv_elem) + len(rows) * self.h * self.dh * 2 * 2 + 4 * pages
+                + 4 * (3 * len(rows) + 1))
 
     def prefill_flops(self) -> int:
         return sum(4 * self.h * self.dh * (n * c + n * (n + 1) // 2) for c, n, _ in self.seqs if n > 1)

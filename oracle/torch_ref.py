@@ -12,6 +12,11 @@ same shapes, so that its rounding is the reference's own:
 
 Runs on any torch device.  On a GPU, callers pass float32 tensors (the bf16 batched-matmul path of
 torch is avoided there); on the CPU it runs in the caller's dtype, exactly as the reference does.
+
+fp8 pools (torch.float8_e4m3fn, the reference's planned fp8 KV cache: docs/distributed_inference_plan.md:310)
+hold e4m3fn(x * (1 / scale)) with one scale per tensor: `write_kv` quantizes with torch's own cast and
+`paged_attention` reads value * scale.  This part has no reference code to follow; it is pinned by
+hand-checked encodings and the e4m3fn grid properties in tests/test_oracle.py.
 """
 
 from __future__ import annotations
@@ -36,11 +41,33 @@ def torch_meta(meta: OracleMetadata, device) -> SimpleNamespace:
     )
 
 
+FP8 = torch.float8_e4m3fn
+
+
+def inv_scale(scale: float) -> float:
+    """1 / scale evaluated in float32 (the value the quantizer multiplies by)."""
+    return (torch.tensor(1.0, dtype=torch.float32) / torch.tensor(scale, dtype=torch.float32)).item()
+
+
+def quantize_fp8(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """e4m3fn(float(x) * (1 / scale)): torch's cast rounds to nearest even and stores NaN for magnitudes
+    above 464 and for non-finite values."""
+    return (x.float() * inv_scale(scale)).to(FP8)
+
+
+def dequantize_fp8(q: torch.Tensor, scale: float, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    return q.to(dtype) * scale
+
+
 def write_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch.Tensor,
-             v: torch.Tensor) -> None:
+             v: torch.Tensor, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
     """Reference `paged_torch_ref.py:23-28`: k, v [N, Hkv, Dh] scattered into the flat pool view at
-    `slot_mapping` [N] (int64), after a cast to the pool's dtype."""
+    `slot_mapping` [N] (int64), after a cast to the pool's dtype (the quantizing cast for an fp8 pool)."""
     hkv, dh = k_cache.shape[-2:]
+    if k_cache.dtype == FP8:  # torch has no index_copy_ for float8: move the bytes
+        k_cache.view(torch.uint8).view(-1, hkv, dh).index_copy_(0, slot_mapping, quantize_fp8(k, k_scale).view(torch.uint8))
+        v_cache.view(torch.uint8).view(-1, hkv, dh).index_copy_(0, slot_mapping, quantize_fp8(v, v_scale).view(torch.uint8))
+        return
     k_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, k.to(k_cache.dtype))
     v_cache.view(-1, hkv, dh).index_copy_(0, slot_mapping, v.to(v_cache.dtype))
 
@@ -60,10 +87,11 @@ def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch
 
 
 def rope_then_write_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                       k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> torch.Tensor:
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                       k_scale: float = 1.0, v_scale: float = 1.0) -> torch.Tensor:
     """The two steps the fused rotary + append replaces: the model's RoPE of q and k
     (`model/llama.py:110`) and `write_kv` of the rotated k and of v.  Returns the rotated q."""
-    write_kv(k_cache, v_cache, slot_mapping, apply_rotary(k, cos, sin), v)
+    write_kv(k_cache, v_cache, slot_mapping, apply_rotary(k, cos, sin), v, k_scale, v_scale)
     return apply_rotary(q, cos, sin)
 
 
@@ -88,11 +116,22 @@ def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torc
 
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
-                    compute_dtype: torch.dtype | None = None) -> torch.Tensor:
+                    compute_dtype: torch.dtype | None = None, k_scale: float = 1.0,
+                    v_scale: float = 1.0) -> torch.Tensor:
     """Reference `paged_torch_ref.py:40-74`.  q [N, H, Dh] -> [N, H, Dh]; the step's own k/v must
     already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`.  With `compute_dtype` the
     gathered context and q are converted to it before SDPA (and the result back to q's dtype): how the
-    oracle runs on a GPU, in float32."""
+    oracle runs on a GPU, in float32.  An fp8 pool's gathered rows are dequantized (value * scale, in
+    `compute_dtype` or q's dtype)."""
+    if getattr(k_cache, "dtype", None) == FP8:
+        cd = compute_dtype or q.dtype
+
+        def deq(scale):
+            return lambda t: dequantize_fp8(t.view(FP8), scale, cd)
+
+        kb, vb = k_cache.view(torch.uint8), v_cache.view(torch.uint8)  # gathered as bytes (no float8 indexing)
+        out = paged_attention(q.to(cd), _Converted(kb, deq(k_scale)), _Converted(vb, deq(v_scale)), meta)
+        return out.to(q.dtype)
     if compute_dtype is not None and compute_dtype != q.dtype:
         orig = q.dtype
 
@@ -134,10 +173,10 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     return out
 
 
-def forward(q, k, v, k_cache, v_cache, meta) -> torch.Tensor:
+def forward(q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0) -> torch.Tensor:
     """Reference `torch_ref.py:46-48`: write the step's k/v into the pool, then attend."""
-    write_kv(k_cache, v_cache, meta.slot_mapping, k, v)
-    return paged_attention(q, k_cache, v_cache, meta)
+    write_kv(k_cache, v_cache, meta.slot_mapping, k, v, k_scale, v_scale)
+    return paged_attention(q, k_cache, v_cache, meta, k_scale=k_scale, v_scale=v_scale)
 
 
 def prefill(q, k, v, key_valid=None) -> torch.Tensor:

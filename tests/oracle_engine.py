@@ -28,9 +28,10 @@ class OracleBackend:
     def __init__(self, compute_dtype=torch.float32) -> None:
         self.compute_dtype = compute_dtype
 
-    def forward(self, q, k, v, k_cache, v_cache, meta):
-        torch_ref.write_kv(k_cache, v_cache, meta.slot_mapping, k, v)
-        return torch_ref.paged_attention(q, k_cache, v_cache, meta, compute_dtype=self.compute_dtype)
+    def forward(self, q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
+        torch_ref.write_kv(k_cache, v_cache, meta.slot_mapping, k, v, k_scale, v_scale)
+        return torch_ref.paged_attention(q, k_cache, v_cache, meta, compute_dtype=self.compute_dtype,
+                                         k_scale=k_scale, v_scale=v_scale)
 
     def prefill(self, q, k, v, key_valid=None, **kwargs):
         dt = q.dtype

@@ -222,3 +222,52 @@ def test_chunked_engine_tokens_equal_unchunked_on_cpu():
     assert chunked == whole and all(len(v) == 12 for v in whole.values())
     mixed = [r for r in core.step_log if r.prefill_tokens and r.decode_tokens]
     assert mixed and max(r.prefill_tokens + r.decode_tokens for r in core.step_log) <= 24
+
+
+def test_fp8_pool_engine_on_cpu():
+    # the engine over an fp8 (e4m3fn) pool with per-tensor scales, oracle hot path on the CPU: it runs
+    # end to end, chunked and whole-prompt prefill give the same tokens, the pool is one byte per
+    # element, and the prefix-cache root is keyed by the pool format and its scales
+    import torch
+
+    from minillm.cache.paged import PagedKVCache
+    from minillm.cache.prefix import root_hash
+    from minillm.engine.core import AddRequest, EngineCore
+    from minillm.model.config import LlamaConfig
+    from minillm.model.llama import LlamaForCausalLM, random_init_
+    from oracle_engine import OracleBackend, oracle_metadata
+
+    cfg = LlamaConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16, rms_norm_eps=1e-5,
+                      rope_theta=10000.0, max_position_embeddings=512)
+    model = LlamaForCausalLM(cfg)
+    random_init_(model, std=0.2, seed=0)
+    model.set_backend(OracleBackend())
+    gen = torch.Generator().manual_seed(2)
+    prompts = [torch.randint(3, 97, (int(n),), generator=gen).tolist() for n in (9, 70, 1, 41)]
+    fp8 = torch.float8_e4m3fn
+
+    def run(**kw):
+        core = EngineCore(model, max_model_len=512, max_batch_size=4, num_kv_blocks=40, metadata_builder=oracle_metadata,
+                          step_log=True, kv_cache_dtype=fp8, kv_scales=(0.5, 0.25), **kw)
+        for i, p in enumerate(prompts):
+            core.add_request(AddRequest(f"r{i}", p, 10, ignore_eos=True))
+        outs = {}
+        while core.has_work():
+            for o in core.step().outputs:
+                outs.setdefault(o.req_id, []).extend(o.new_token_ids)
+            core.check_blocks()
+        return outs, core
+
+    whole, core = run()
+    chunked, _ = run(chunked_prefill=True, max_num_batched_tokens=16)
+    assert chunked == whole and all(len(v) == 10 for v in whole.values())
+    assert core.cache.k[0].dtype == fp8 and core.cache.scales(1) == {"k_scale": 0.5, "v_scale": 0.25}
+    assert core.cache.k[0].view(torch.uint8).any()  # something was written
+    assert PagedKVCache.bytes_per_block(cfg, fp8) * 2 == PagedKVCache.bytes_per_block(cfg, torch.float32) // 2
+    keys = dict(core._salt_keys)
+    assert keys["kv_dtype"] == "float8_e4m3fn" and keys["kv_scales"] == [0.5, 0.25]
+    plain = {k: v for k, v in keys.items() if k != "kv_scales"} | {"kv_dtype": "bfloat16"}
+    assert root_hash({**keys, "salt": ""}) != root_hash({**plain, "salt": ""})
+    with pytest.raises(ValueError, match="fp8 pools only"):
+        PagedKVCache(cfg, 4, "cpu", torch.bfloat16, k_scale=2.0)

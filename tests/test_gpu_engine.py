@@ -175,3 +175,22 @@ def test_chunked_prefill_engine_matches_oracle(hip):
     assert_greedy_match(got, exp)
     mixed = [r for r in core.step_log if r.prefill_tokens and r.decode_tokens]
     assert mixed and max(r.prefill_tokens + r.decode_tokens for r in core.step_log) <= 96
+
+
+def test_fp8_pool_engine_matches_oracle(hip):
+    # an fp8 (e4m3fn) pool with per-tensor scales, fused RoPE + quantizing append, fp8 decode and prefill,
+    # with preemption and prefix sharing, against the oracle engine on an fp8 pool of the same format
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+
+    model = tiny_model(seed=21)
+    head = prompts(1, 40, 41, seed=22)[0]
+    ps = [head + p for p in prompts(8, 1, 300, seed=23)]
+    kw = dict(max_batch_size=6, num_kv_blocks=64, max_model_len=4096, kv_cache_dtype=torch.float8_e4m3fn,
+              kv_scales=(0.5, 0.25))
+    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 24, **kw)
+    exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 24, **kw)
+    assert_greedy_match(got, exp)
+    assert core.cache.k[0].dtype == torch.float8_e4m3fn
+    st = core.stats()
+    assert st.num_preemptions > 0 and st.prefix_cache_hits > 0

@@ -325,3 +325,104 @@ def test_rope_then_write_kv_writes_rotated_k_and_plain_v():
     assert q_rot.shape == q.shape
     untouched = sorted(set(range(nb * bs)) - set(slots.tolist()))
     assert torch.count_nonzero(flat_k[untouched]) == 0 and torch.count_nonzero(flat_v[untouched]) == 0
+
+
+# ---------------------------------------------------------------- fp8 (e4m3fn) pool
+
+
+def e4m3fn_value(code: int) -> float:
+    """OCP e4m3fn decoded from its bit fields: 1 sign, 4 exponent (bias 7) and 3 mantissa bits; exponent
+    0 is subnormal (m / 8 * 2^-6); S.1111.111 is NaN; there are no infinities."""
+    s, e, m = code >> 7, (code >> 3) & 15, code & 7
+    if e == 15 and m == 7:
+        return math.nan
+    mag = (m / 8) * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+    return -mag if s else mag
+
+
+def fp8_bytes(x: torch.Tensor, scale: float = 1.0) -> list[int]:
+    return torch_ref.quantize_fp8(x, scale).view(torch.uint8).tolist()
+
+
+def test_fp8_encodings_by_hand():
+    x = torch.tensor([1.0, -1.5, 0.1, 448.0, 464.0, 465.0, 480.0, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -10, 0.0, -0.0,
+                      math.inf, -math.inf, math.nan, -465.0])
+    assert fp8_bytes(x) == [0x38, 0xBC, 0x1D, 0x7E, 0x7E, 0x7F, 0x7F, 0x01, 0x00, 0x01, 0x00, 0x80, 0x7F, 0xFF, 0x7F,
+                            0xFF]
+    # the stored value is x * (1 / scale): 3 / 2 = 1.5 -> 0x3C, 1 / 0.25 = 4 -> 0x48
+    assert fp8_bytes(torch.tensor([3.0]), 2.0) == [0x3C]
+    assert fp8_bytes(torch.tensor([1.0]), 0.25) == [0x48]
+    assert torch_ref.inv_scale(3.0) == np.float32(1.0) / np.float32(3.0)
+
+
+def test_fp8_decoding_matches_the_bit_fields():
+    got = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch_ref.FP8).float().tolist()
+    for code, value in enumerate(got):
+        exp = e4m3fn_value(code)
+        assert (math.isnan(exp) and math.isnan(value)) or exp == value, hex(code)
+
+
+def test_fp8_quantize_is_round_to_nearest_even_on_the_grid():
+    finite = [c for c in range(256) if not math.isnan(e4m3fn_value(c))]
+    # every finite code is its own encoding
+    assert fp8_bytes(torch.tensor([e4m3fn_value(c) for c in finite])) == finite
+    pos = list(range(0x7F))  # non-negative finite codes, increasing with value
+    grid = [e4m3fn_value(c) for c in pos]
+    # midpoints of neighbours: the even code wins
+    mids = torch.tensor([(grid[i] + grid[i + 1]) / 2 for i in range(len(grid) - 1)])
+    assert fp8_bytes(mids) == [pos[i] if pos[i] % 2 == 0 else pos[i + 1] for i in range(len(grid) - 1)]
+    # brute force: the nearest grid value of log-uniform magnitudes; above 464 the cast gives NaN
+    g = torch.Generator().manual_seed(0)
+    mag = torch.exp2(torch.rand(20000, generator=g) * 21 - 12)  # 2^-12 .. 2^9
+    sign = torch.where(torch.rand(20000, generator=g) < 0.5, -1.0, 1.0)
+    xs = (mag * sign).float()
+    got = fp8_bytes(xs)
+    for x, code in zip(xs.tolist(), got):
+        a = abs(x)
+        if a > 464:
+            exp = 0x7F
+        else:
+            d = [abs(a - v) for v in grid]
+            best = min(d)
+            ties = [pos[i] for i, di in enumerate(d) if di == best]
+            exp = next(c for c in ties if c % 2 == 0) if len(ties) > 1 else ties[0]
+        if x < 0:
+            exp |= 0x80
+        assert code == exp, (x, hex(code), hex(exp))
+
+
+def test_fp8_write_kv_quantizes_into_its_slots_only():
+    g = torch.Generator().manual_seed(4)
+    kc = torch.zeros(6, 4, 2, 8, dtype=torch_ref.FP8)
+    vc = torch.zeros_like(kc)
+    k, v = torch.randn(7, 2, 8, generator=g) * 3, torch.randn(7, 2, 8, generator=g) * 0.1
+    slots = torch.tensor([21, 22, 23, 20, 5, 4, 6])
+    torch_ref.write_kv(kc, vc, slots, k, v, k_scale=2.0, v_scale=0.05)
+    fk, fv = kc.view(torch.uint8).view(-1, 2, 8), vc.view(torch.uint8).view(-1, 2, 8)
+    assert torch.equal(fk[slots], torch_ref.quantize_fp8(k, 2.0).view(torch.uint8))
+    assert torch.equal(fv[slots], torch_ref.quantize_fp8(v, 0.05).view(torch.uint8))
+    keep = torch.ones(24, dtype=torch.bool)
+    keep[slots] = False
+    assert torch.count_nonzero(fk[keep]) == 0 and torch.count_nonzero(fv[keep]) == 0
+    # dequantized, each value is within half a grid step of the input (3 mantissa bits: 2^-4 relative)
+    back = torch_ref.dequantize_fp8(kc.view(-1, 2, 8)[slots], 2.0)
+    assert torch.all((back - k).abs() <= 2.0 ** -4 * k.abs() + 2.0 * 2.0 ** -10)
+
+
+def test_fp8_paged_attention_equals_textbook_over_dequantized_context():
+    case = cases()["paged_equals_dense"]
+    q, k, v, pool_k, pool_v, meta, seqs, ctx_k, ctx_v = build_step(case)
+    ks, vs = 0.5, 0.125  # distinct, so swapping K's and V's scales fails
+    k8, v8 = (torch.zeros(pool_k.shape, dtype=torch_ref.FP8) for _ in range(2))
+    for i, s in enumerate(seqs):
+        slots = torch.tensor([s.block_ids[p // case["bs"]] * case["bs"] + p % case["bs"] for p in range(s.num_cached)],
+                             dtype=torch.long)
+        torch_ref.write_kv(k8, v8, slots, ctx_k[i][:s.num_cached], ctx_v[i][:s.num_cached], ks, vs)
+    out = torch_ref.forward(q, k, v, k8, v8, torch_ref.torch_meta(meta, "cpu"), k_scale=ks, v_scale=vs)
+    for i, s in enumerate(seqs):
+        st, n, length = meta.query_start_loc[i], s.num_new, meta.seq_lens[i]
+        dk = torch_ref.dequantize_fp8(torch_ref.quantize_fp8(ctx_k[i], ks), ks)
+        dv = torch_ref.dequantize_fp8(torch_ref.quantize_fp8(ctx_v[i], vs), vs)
+        exp = naive_attention(q[st:st + n].transpose(0, 1), dk.transpose(0, 1), dv.transpose(0, 1),
+                              causal_allowed(n, length))
+        torch.testing.assert_close(out[st:st + n].double(), exp.transpose(0, 1), atol=1e-5, rtol=1e-5)
