@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--chunked-prefill", action="store_true",
                     help="engine_8b: mixed steps (decode rows + prompt chunks under the token budget)")
     ap.add_argument("--max-num-batched-tokens", type=int, default=8192)
+    ap.add_argument("--decode-graphs", action="store_true",
+                    help="engine_8b: run pure decode steps as captured HIP graphs (batch buckets 1..128)")
     ap.add_argument("--kv-dtype", choices=["bf16", "fp8"], default="bf16",
                     help="KV pool format: bf16 (the reference's) or fp8 e4m3fn with per-tensor scales")
     return ap.parse_args()
@@ -166,7 +168,8 @@ def bench_engine(args):
         core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=args.requests,
                           num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder,
                           chunked_prefill=args.chunked_prefill, max_num_batched_tokens=args.max_num_batched_tokens,
-                          kv_cache_dtype=torch.float8_e4m3fn if args.kv_dtype == "fp8" else None)
+                          kv_cache_dtype=torch.float8_e4m3fn if args.kv_dtype == "fp8" else None,
+                          decode_graphs=args.decode_graphs and backend is hip_backend)
         for i, p in enumerate(prompts):
             core.add_request(AddRequest(f"r{i}", p, args.decode_steps, ignore_eos=True))
         out, margins, last = {}, {}, {}
@@ -205,7 +208,8 @@ def bench_engine(args):
                                             "rotary": "torch" if args.unfused_rotary else "fused into the KV append",
                                             "scheduling": (f"chunked prefill, {args.max_num_batched_tokens}-token steps"
                                                            if args.chunked_prefill else "prefill-first"),
-                                            "kv_dtype": "fp8_e4m3fn (scales 1)" if args.kv_dtype == "fp8" else "bf16"},
+                                            "kv_dtype": "fp8_e4m3fn (scales 1)" if args.kv_dtype == "fp8" else "bf16",
+                                            "decode_steps_as": "HIP graphs" if args.decode_graphs else "eager launches"},
             "engine": {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}}
     if args.compare_oracle:
         from oracle_engine import OracleBackend, oracle_metadata

@@ -114,6 +114,18 @@ int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_se
               int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work,
               int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work, void* stream);
 
+/*
+ * mllm_plan with the split size read from device memory at run time (*pages_per_split, clamped to
+ * [min_pages_per_split, 128]).  No counterpart in the reference: it serves HIP-graph capture of decode steps
+ * (the reference's planned M8, docs/distributed_inference_plan.md:309), where one captured plan launch
+ * re-plans every replayed step.  The capacities must cover min_pages_per_split splits, so no item is ever
+ * dropped; items past a step's own stay as the caller pre-filled them (-1).
+ */
+int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, const int32_t* pages_per_split,
+                  int32_t min_pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
+                  int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work,
+                  void* stream);
+
 /* Bytes of fp32 split-KV partials the decode needs for num_decode_work items (0 if none split). */
 int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim);
 

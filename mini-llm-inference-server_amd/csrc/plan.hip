@@ -41,15 +41,20 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* sums, int* total) {
   return prefix + x - v;
 }
 
+// split_dev: when not null, the split size is read from device memory (clamped to [pages_per_split, 128]:
+// the capacities were sized for pages_per_split, so no item is ever dropped).
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ qo_indptr,
                                                             const int32_t* __restrict__ kv_indptr, int32_t num_seqs,
-                                                            int32_t pages_per_split, int32_t q_tile,
+                                                            int32_t pages_per_split_arg,
+                                                            const int32_t* __restrict__ split_dev, int32_t q_tile,
                                                             int4* __restrict__ decode_work, int32_t cap_decode,
                                                             int4* __restrict__ merge_work, int32_t cap_merge,
                                                             int2* __restrict__ prefill_work, int32_t cap_prefill) {
   __shared__ int sums[kPlanThreads / 64];
   __shared__ int hist[kMaxSplitPages + 1];  // decode items per size in pages
   __shared__ int offs[kMaxSplitPages + 1];  // next free position of each size class
+  const int pages_per_split =
+      split_dev ? min(max(*split_dev, pages_per_split_arg), kMaxSplitPages) : pages_per_split_arg;
   for (int i = threadIdx.x; i <= kMaxSplitPages; i += blockDim.x) hist[i] = 0;
   __syncthreads();
   // pass 1: sizes of the decode items.  A row of P pages gets ns = ceil(P / C) splits of P / ns pages
@@ -110,25 +115,48 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
 }  // namespace
 }  // namespace mllm
 
+namespace {
+
+int plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, int32_t pages_per_split,
+         const int32_t* split_dev, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
+         int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work, void* stream,
+         const char* fn) {
+  using namespace mllm;
+  const std::string f = fn;
+  MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, f + ": num_seqs < 0");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
+               f + ": pages_per_split must be in [1, 128]");
+  MLLM_REQUIRE(q_tile_tokens >= 1, MLLM_ERR_INVALID, f + ": q_tile_tokens must be positive");
+  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0 && num_prefill_work >= 0, MLLM_ERR_INVALID,
+               f + ": negative capacity");
+  MLLM_REQUIRE((num_decode_work == 0 || decode_work) && (num_merge_work == 0 || merge_work) &&
+                   (num_prefill_work == 0 || prefill_work),
+               MLLM_ERR_INVALID, f + ": null work buffer");
+  if (num_seqs == 0) return MLLM_OK;
+  MLLM_REQUIRE(qo_indptr && kv_indptr, MLLM_ERR_INVALID, f + ": null indptr");
+  plan_kernel<<<1, kPlanThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      qo_indptr, kv_indptr, num_seqs, pages_per_split, split_dev, q_tile_tokens, reinterpret_cast<int4*>(decode_work),
+      num_decode_work, reinterpret_cast<int4*>(merge_work), num_merge_work, reinterpret_cast<int2*>(prefill_work),
+      num_prefill_work);
+  return check_launch(fn);
+}
+
+}  // namespace
+
 extern "C" int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs,
                          int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work,
                          int32_t num_decode_work, int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work,
                          int32_t num_prefill_work, void* stream) {
+  return plan(qo_indptr, kv_indptr, num_seqs, pages_per_split, nullptr, q_tile_tokens, decode_work, num_decode_work,
+              merge_work, num_merge_work, prefill_work, num_prefill_work, stream, "mllm_plan");
+}
+
+extern "C" int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs,
+                             const int32_t* pages_per_split, int32_t min_pages_per_split, int32_t q_tile_tokens,
+                             int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work,
+                             int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work, void* stream) {
   using namespace mllm;
-  MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, "mllm_plan: num_seqs < 0");
-  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
-               "mllm_plan: pages_per_split must be in [1, 128]");
-  MLLM_REQUIRE(q_tile_tokens >= 1, MLLM_ERR_INVALID, "mllm_plan: q_tile_tokens must be positive");
-  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0 && num_prefill_work >= 0, MLLM_ERR_INVALID,
-               "mllm_plan: negative capacity");
-  MLLM_REQUIRE((num_decode_work == 0 || decode_work) && (num_merge_work == 0 || merge_work) &&
-                   (num_prefill_work == 0 || prefill_work),
-               MLLM_ERR_INVALID, "mllm_plan: null work buffer");
-  if (num_seqs == 0) return MLLM_OK;
-  MLLM_REQUIRE(qo_indptr && kv_indptr, MLLM_ERR_INVALID, "mllm_plan: null indptr");
-  plan_kernel<<<1, kPlanThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      qo_indptr, kv_indptr, num_seqs, pages_per_split, q_tile_tokens, reinterpret_cast<int4*>(decode_work),
-      num_decode_work, reinterpret_cast<int4*>(merge_work), num_merge_work, reinterpret_cast<int2*>(prefill_work),
-      num_prefill_work);
-  return check_launch("mllm_plan");
+  MLLM_REQUIRE(pages_per_split, MLLM_ERR_INVALID, "mllm_plan_dev: null pages_per_split");
+  return plan(qo_indptr, kv_indptr, num_seqs, min_pages_per_split, pages_per_split, q_tile_tokens, decode_work,
+              num_decode_work, merge_work, num_merge_work, prefill_work, num_prefill_work, stream, "mllm_plan_dev");
 }

@@ -34,6 +34,7 @@ SIGNATURES = {
     "mllm_rope_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32, _i32,
                                            _i32, _i32, _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p]),
     "mllm_plan": (ctypes.c_int, [_p, _p, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
+    "mllm_plan_dev": (ctypes.c_int, [_p, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
     "mllm_decode_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32]),
     "mllm_paged_decode": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                          _i32, _p, _i32, _i32, _f32, _i32, _p, _i64, _i64, _p, _i64, _p]),

@@ -164,6 +164,17 @@ class HipBackend(AttentionBackend):
                        _native.dtype_code(k_cache.dtype), num_blocks * bs, hkv, dh, meta.slot_mapping.data_ptr(),
                        k.shape[0], _native.stream_ptr(k_cache.device))
 
+    def detach_workspace(self) -> torch.Tensor | None:
+        """Hands the decode workspace to the caller and starts a new one on the next use (a captured HIP
+        graph keeps the buffer it recorded, whatever later eager steps allocate)."""
+        ws, self._workspace = self._workspace, None
+        return ws
+
+    def invalidate_plan(self) -> None:
+        """Forget the cached plan: the next layer builds one even for a `meta` it has seen (HIP-graph
+        capture records that build, so every replay re-plans from the staged metadata)."""
+        self._planned = None
+
     def plan(self, meta, num_heads: int, num_kv_heads: int, head_dim: int, device) -> StepPlan:
         """The step's work plan, built on the GPU once per `meta` object and reused after."""
         if self._planned is not meta:
@@ -223,7 +234,10 @@ class HipBackend(AttentionBackend):
         news, lens, bs = meta.num_new, meta.seq_lens, meta.block_size
         pages = [-(-length // bs) for length in lens]
         decode_pages = sum(p for p, nn in zip(pages, news) if nn == 1)
-        c = pages_per_split(decode_pages, hkv)
+        # a graph-captured step (StaticDecodeMetadata) stages its split size on the device; the
+        # capacities then cover the smallest split it may stage
+        split_dev = getattr(meta, "split_dev", None)
+        c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv)
         g = h // hkv
         q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
         n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
@@ -231,8 +245,13 @@ class HipBackend(AttentionBackend):
         n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
         buf = torch.full((4 * n_dec + 4 * n_merge + 2 * n_pf,), -1, dtype=torch.int32, device=dev)
         dec, mrg, pf = buf[:4 * n_dec], buf[4 * n_dec:4 * (n_dec + n_merge)], buf[4 * (n_dec + n_merge):]
-        self._lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs, c, q_tile,
-                       _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf, stream)
+        if split_dev is not None:
+            self._lib.call("mllm_plan_dev", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs,
+                           split_dev.data_ptr(), c, q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf,
+                           stream)
+        else:
+            self._lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs, c,
+                           q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf, stream)
         ws = self._lib.workspace_bytes(n_dec, h, dh) if n_merge else 0
         self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws)
         self._planned = meta

@@ -87,12 +87,14 @@ class EngineCore:
                  max_num_batched_tokens: int | None = None, num_kv_blocks: int | None = None,
                  enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None,
                  chunked_prefill: bool = False, kv_cache_dtype: torch.dtype | None = None,
-                 kv_scales: tuple[float, float] = (1.0, 1.0)) -> None:
+                 kv_scales: tuple[float, float] = (1.0, 1.0), decode_graphs=None) -> None:
         """`metadata_builder(seqs, block_size, device)` defaults to AttentionMetadata.build (the GPU
         build); a test may pass another implementation of the same contract.  `chunked_prefill` mixes
         decode rows and prompt chunks in one step under the token budget (see Scheduler).
         `kv_cache_dtype` defaults to the model's dtype; torch.float8_e4m3fn gives an fp8 pool whose K and
-        V tensors of every layer use the per-tensor scales `kv_scales` (k_scale, v_scale)."""
+        V tensors of every layer use the per-tensor scales `kv_scales` (k_scale, v_scale).
+        `decode_graphs` (True, or a tuple of batch buckets) runs pure decode steps as captured HIP graphs
+        (DecodeGraphs); prefill and mixed steps stay eager."""
         self.model = model
         self.build_metadata = metadata_builder or AttentionMetadata.build
         p = next(model.parameters())
@@ -112,6 +114,12 @@ class EngineCore:
                            "layout": "NHD", "model": model_id}
         if self.cache.quantized:  # the stored bytes depend on the scales too
             self._salt_keys["kv_scales"] = [kv_scales[0], kv_scales[1]]
+        self.graphs = None
+        if decode_graphs:
+            from .graphs import DEFAULT_BUCKETS, DecodeGraphs
+
+            buckets = DEFAULT_BUCKETS if decode_graphs is True else tuple(decode_graphs)
+            self.graphs = DecodeGraphs(model, self.cache, self.max_model_len, BLOCK_SIZE, buckets)
         self.step_log: list[StepRecord] | None = [] if step_log else None
         self._step = 0
         self._aborted: list[RequestOutput] = []
@@ -170,11 +178,14 @@ class EngineCore:
         for r in plan.prefill:
             r.timeline.setdefault("scheduled", t0)
         new = [r.uncached()[:n] for r, n in rows]
-        meta = self.build_metadata([SeqStep(r.num_cached, len(n), r.block_ids) for r, n in zip(reqs, new)],
-                                   BLOCK_SIZE, self.device)
-        ids = torch.tensor([[t for n in new for t in n]], device=self.device)
-        logits = self.model(ids, kv_cache=self.cache.step(meta), last_index=meta.logits_index)
-        tokens = logits[:, -1].argmax(dim=-1).tolist()
+        seqs = [SeqStep(r.num_cached, len(n), r.block_ids) for r, n in zip(reqs, new)]
+        if self.graphs is not None and not plan.prefill and self.graphs.supports(len(seqs)):
+            tokens = self.graphs.run(seqs, [n[0] for n in new])
+        else:
+            meta = self.build_metadata(seqs, BLOCK_SIZE, self.device)
+            ids = torch.tensor([[t for n in new for t in n]], device=self.device)
+            logits = self.model(ids, kv_cache=self.cache.step(meta), last_index=meta.logits_index)
+            tokens = logits[:, -1].argmax(dim=-1).tolist()
         t_tok = now_ns()
         done = []
         for req, n, token in zip(reqs, new, tokens):

@@ -1,0 +1,137 @@
+"""HIP-graph capture of decode steps (the reference's planned M8, "CUDA graphs for decode":
+docs/distributed_inference_plan.md:309; the plan-once/run-per-layer split it relies on is FlashInfer's,
+src/minillm/attention/flashinfer_backend.py:44).
+
+A decode step launches about fifteen kernels per layer; at small batch the host's work to launch them
+exceeds the GPU's time.  For each batch bucket B, `DecodeGraphs` captures everything a decode step does
+after the scheduler has picked its rows into one HIP graph over fixed device buffers:
+  the metadata build (mllm_build_metadata), the work plan (a -1 fill and mllm_plan), the model forward
+  (embedding, 32 x {RMSNorm, QKV GEMM, fused RoPE + KV append, split-KV decode + merge, o_proj, MLP}),
+  lm_head on the B last positions and the greedy argmax.
+A step then costs the host one packed upload of (num_cached, num_new, block tables), one input-id copy,
+one graph launch and the read of B token ids.
+
+The graph is captured with worst-case sizes: every row may hold up to ceil(max_model_len / block_size)
+blocks, so the plan's capacities cover B rows at that length split into the smallest splits, and the
+plan slots a step leaves unused stay -1, which every kernel skips.  Each replay stages the split size
+an eager step of the same rows would use (mllm_plan_dev reads it on the device), so a replayed step
+runs the same decode work as the eager one.  Rows past the step's own are padding (see
+StaticDecodeMetadata).
+Only pure decode steps run as graphs; prefill and mixed steps run eagerly.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..attention.hip_backend import pages_per_split
+from ..attention.metadata import SeqStep, StaticDecodeMetadata
+
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
+
+
+class _Captured:
+    def __init__(self, static: StaticDecodeMetadata, ids: torch.Tensor, pinned_ids: torch.Tensor) -> None:
+        self.static, self.ids, self.pinned_ids = static, ids, pinned_ids
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.workspace: torch.Tensor | None = None  # the decode workspace the graph recorded
+        self.logits: torch.Tensor | None = None  # [B, V] of the last replay
+        self.tokens: torch.Tensor | None = None  # [B] greedy ids of the last replay
+
+
+class DecodeGraphs:
+    """Captured decode steps of `model` over `cache`, one graph per bucket, captured on first use."""
+
+    def __init__(self, model, cache, max_model_len: int, block_size: int, buckets=DEFAULT_BUCKETS) -> None:
+        backend = model.model.layers[0].self_attn.backend
+        if not hasattr(backend, "invalidate_plan"):
+            raise ValueError("decode graphs need the hip attention backend")
+        self.model, self.cache, self.backend = model, cache, backend
+        self.block_size = block_size
+        self.max_blocks = -(-max_model_len // block_size)
+        self.buckets = tuple(sorted(set(int(b) for b in buckets)))
+        self.device = next(model.parameters()).device
+        self.num_kv_heads = model.config.num_key_value_heads
+        self._captured: dict[int, _Captured] = {}
+        self._pool = None
+        self.replays = 0
+        self.last_bucket: int | None = None
+
+    def supports(self, num_rows: int) -> bool:
+        return 0 < num_rows <= self.buckets[-1]
+
+    def bucket(self, num_rows: int) -> int:
+        return next(b for b in self.buckets if b >= num_rows)
+
+    def run(self, seqs: list[SeqStep], token_ids: list[int]) -> list[int]:
+        """One decode step: `seqs` are the rows (one new token each, its id in `token_ids`).  Returns each
+        row's greedy next token."""
+        b = self.bucket(len(seqs))
+        c = self.captured(b)
+        self._stage(c, seqs, token_ids)
+        c.graph.replay()
+        self.replays += 1
+        self.last_bucket = b
+        return c.tokens[:len(seqs)].tolist()
+
+    def captured(self, bucket: int) -> _Captured:
+        if bucket not in self._captured:
+            self._captured[bucket] = self._capture(bucket)
+        return self._captured[bucket]
+
+    # ------------------------------------------------------------------ internals
+
+    def _stage(self, c: _Captured, seqs: list[SeqStep], token_ids: list[int]) -> None:
+        bs = self.block_size
+        pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs)
+        c.static.load(seqs, pages_per_split(pages, self.num_kv_heads))  # the eager step's split size
+        ids = c.pinned_ids.numpy()
+        ids[:len(token_ids)] = token_ids
+        ids[len(token_ids):] = 0
+        c.ids.copy_(c.pinned_ids.view(1, -1), non_blocking=True)
+
+    def _body(self, c: _Captured):
+        """The captured work: metadata build, then the forward (whose first layer builds the plan)."""
+        c.static.build()
+        self.backend.invalidate_plan()
+        meta = c.static.meta
+        logits = self.model(c.ids, kv_cache=self.cache.step(meta), last_index=meta.logits_index)[:, -1]
+        return logits, logits.argmax(dim=-1)
+
+    @torch.inference_mode()
+    def _capture(self, bucket: int) -> _Captured:
+        static = StaticDecodeMetadata(bucket, self.max_blocks, self.block_size, self.device)
+        c = _Captured(static, torch.zeros((1, bucket), dtype=torch.long, device=self.device),
+                      torch.zeros(bucket, dtype=torch.long, pin_memory=True))
+        self._stage(c, [], [])  # every row padding: a valid step that writes nothing to the pool
+        # warm-up on a side stream (sizes a fresh workspace for the worst-case plan), then capture
+        self.backend.detach_workspace()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._body(c)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        c.graph = torch.cuda.CUDAGraph()
+        if self._pool is None:
+            self._pool = torch.cuda.graph_pool_handle()
+        with torch.cuda.graph(c.graph, pool=self._pool):
+            c.logits, c.tokens = self._body(c)
+        c.workspace = self.backend.detach_workspace()  # owned by the graph from now on
+        self.backend.invalidate_plan()  # eager steps must not reuse the captured plan buffers
+        torch.cuda.synchronize(self.device)
+        return c
+
+    def eager_reference(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The last replayed step run again eagerly on the same staged inputs (for tests: the replay must
+        equal it).  It appends the same k/v rows at the same slots again."""
+        c = self._captured[self.last_bucket]
+        with torch.inference_mode():
+            eager_ws, self.backend._workspace = self.backend._workspace, c.workspace
+            try:
+                out = self._body(c)
+            finally:
+                self.backend._workspace = eager_ws
+                self.backend.invalidate_plan()
+            return out

@@ -1,0 +1,72 @@
+"""Decode steps as captured HIP graphs (DecodeGraphs): every replay equals the same step run eagerly, bit
+for bit, with eager steps (prefills, other buckets) and synchronisations between replays; and the engine
+with graphs gives the eager engine's greedy tokens, on bf16 and fp8 pools."""
+
+import pytest
+import torch
+
+from test_gpu_engine import assert_greedy_match, prompts, run_engine, tiny_model
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _engine(model, **kw):
+    from minillm.engine.core import EngineCore
+
+    return EngineCore(model, max_batch_size=8, num_kv_blocks=200, max_model_len=2048, **kw)
+
+
+def test_every_replay_equals_the_eager_step(hip):
+    # after every replay the same step runs eagerly on the same staged inputs; prefill steps (eager) and
+    # replays of other buckets come in between as the batch fills and drains
+    from minillm.attention import get_backend
+    from minillm.engine.core import AddRequest
+
+    model = tiny_model(seed=31)
+    model.set_backend(get_backend("hip"))
+    core = _engine(model, decode_graphs=(2, 8))
+    for i, (p, n) in enumerate(zip(prompts(5, 1, 200, seed=32), (4, 7, 9, 30, 40))):
+        core.add_request(AddRequest(f"r{i}", p, n, ignore_eos=True))  # the batch drains from 5 rows to 1
+    seen, buckets = 0, set()
+    while core.has_work():
+        core.step()
+        if core.graphs.replays == seen:
+            continue
+        seen = core.graphs.replays
+        c = core.graphs._captured[core.graphs.last_bucket]
+        got_logits, got_tokens = c.logits.clone(), c.tokens.clone()
+        ref_logits, ref_tokens = core.graphs.eager_reference()
+        torch.cuda.synchronize()
+        assert torch.equal(got_tokens, ref_tokens), core.graphs.last_bucket
+        assert torch.equal(got_logits.view(torch.int16), ref_logits.view(torch.int16)), core.graphs.last_bucket
+        buckets.add(core.graphs.last_bucket)
+    assert seen >= 30 and buckets == {2, 8}
+
+
+@pytest.mark.parametrize("kv", ["fp16", "fp8"])
+def test_graph_engine_matches_eager_engine(hip, kv):
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+
+    model = tiny_model(seed=41)
+    ps = prompts(11, 1, 300, seed=42)
+    kw = dict(max_batch_size=8, num_kv_blocks=300, max_model_len=2048)
+    if kv == "fp8":
+        kw.update(kv_cache_dtype=torch.float8_e4m3fn, kv_scales=(0.5, 0.25))
+    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, decode_graphs=True, **kw)
+    exp, _ = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, **kw)
+    assert_greedy_match(got, exp)
+    assert core.graphs.replays > 10 and len(core.graphs._captured) >= 2  # batch shrinks as requests finish
+
+
+def test_graph_rejects_what_it_cannot_hold(hip):
+    from minillm.attention.metadata import SeqStep, StaticDecodeMetadata
+
+    sm = StaticDecodeMetadata(4, 8, 16, DEV)
+    with pytest.raises(ValueError, match="decode graph"):
+        sm.load([SeqStep(0, 1, [1])] * 5)
+    with pytest.raises(ValueError, match="one new token"):
+        sm.load([SeqStep(0, 2, [1])])
+    with pytest.raises(ValueError, match="exceeds"):
+        sm.load([SeqStep(200, 1, list(range(13)))])

@@ -113,3 +113,15 @@ def test_workloads_are_deterministic_and_sized():
     assert a.algorithmic_bytes() == 3_604_480 + 65_536 + 32_768 + 232 + 4 * 13
     used = [b for _, _, t in a.seqs for b in t]
     assert len(set(used)) == len(used) and max(used) < a.num_blocks
+
+
+def test_packed_step_upload_layout():
+    # num_cached[S] | num_new[S] | table_indptr[S+1] | table_ids: the one upload the GPU build reads
+    import numpy as np
+
+    from minillm.attention.metadata import SeqStep, pack_steps
+
+    out = np.full(16, 99, dtype=np.int32)
+    got = pack_steps([SeqStep(3, 1, [7]), SeqStep(0, 5, [2, 9])], out)
+    assert got.tolist() == [3, 0, 1, 5, 0, 1, 3, 7, 2, 9]
+    assert out[10:].tolist() == [99] * 6  # nothing written past the packed step
