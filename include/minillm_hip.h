@@ -66,6 +66,28 @@ int mllm_build_metadata(const int32_t* num_cached, const int32_t* num_new, const
                         int32_t* kv_indices, int32_t* kv_last_page_len, void* stream);
 
 /*
+ * The same build from a device-resident mirror of the block manager's tables (the reference rebuilds
+ * and uploads every table each step, metadata.py:82-83,101):
+ * tables[rows x table_stride] holds one request per row; sequence s of the step reads row seq_rows[s],
+ * whose first seq_num_blocks[s] entries are its block_ids.  Only num_cached, num_new, seq_rows and
+ * seq_num_blocks travel with the step.  Outputs as mllm_build_metadata, bit-identical.
+ */
+int mllm_build_metadata_rows(const int32_t* num_cached, const int32_t* num_new, const int32_t* seq_rows,
+                             const int32_t* seq_num_blocks, const int32_t* tables, int32_t table_stride,
+                             int32_t num_seqs, int32_t block_size, int32_t table_width, int64_t* positions,
+                             int64_t* slot_mapping, int64_t* block_tables, int64_t* logits_index, int32_t* qo_indptr,
+                             int32_t* seq_lens, int32_t* block_tables_i32, int32_t* kv_indptr, int32_t* kv_indices,
+                             int32_t* kv_last_page_len, void* stream);
+
+/*
+ * Keeps the resident mirror current: for i < num_updates, tables[updates[2 i]] = updates[2 i + 1] (flat
+ * index, block id); indices outside [0, table_size) are skipped.  The step's newly allocated blocks
+ * are its only updates, so a decode step sends a few ids instead of every table.
+ */
+int mllm_update_block_tables(int32_t* tables, int64_t table_size, const int32_t* updates, int32_t num_updates,
+                             void* stream);
+
+/*
  * KV append: scatter N new K and V rows into the pool at slot_mapping.
  * Replaces write_kv (reference src/minillm/attention/paged_torch_ref.py:23-28), i.e.
  *   k_cache.view(-1, Hkv, Dh).index_copy_(0, slot_mapping, k.to(k_cache.dtype)), same for v.

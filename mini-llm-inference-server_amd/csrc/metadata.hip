@@ -5,7 +5,9 @@
 //   logits_index.
 // Launch 2 (one workgroup per sequence): the per-token fields (positions, slot_mapping), the padded
 //   block-table row (int64 and int32) and the sequence's page list (kv_indices), all written with
-//   coalesced stores from the CSR copy of the block manager's tables.
+//   coalesced stores from the block manager's tables: either a CSR copy uploaded with the step
+//   (mllm_build_metadata) or a device-resident mirror with one row per request, read through the step's
+//   row ids (mllm_build_metadata_rows), which the caller keeps current with mllm_update_block_tables.
 #include "common.h"
 
 namespace mllm {
@@ -75,21 +77,32 @@ __global__ __launch_bounds__(kScanThreads) void metadata_scan_kernel(
   }
 }
 
+// Tables: CSR (table_indptr[S+1] into table_ids) when seq_rows is null; otherwise sequence s reads row
+// seq_rows[s] of the resident mirror table_ids[rows x table_stride], of which its first seq_nblk[s] entries
+// are its table.
 __global__ __launch_bounds__(256) void metadata_fill_kernel(
     const int32_t* __restrict__ num_cached, const int32_t* __restrict__ num_new,
-    const int32_t* __restrict__ table_indptr, const int32_t* __restrict__ table_ids, int32_t block_size,
-    int32_t table_width, const int32_t* __restrict__ qo_indptr, const int32_t* __restrict__ kv_indptr,
-    int64_t* __restrict__ positions, int64_t* __restrict__ slot_mapping, int64_t* __restrict__ block_tables,
-    int32_t* __restrict__ block_tables_i32, int32_t* __restrict__ kv_indices) {
+    const int32_t* __restrict__ table_indptr, const int32_t* __restrict__ table_ids,
+    const int32_t* __restrict__ seq_rows, const int32_t* __restrict__ seq_nblk, int32_t table_stride,
+    int32_t block_size, int32_t table_width, const int32_t* __restrict__ qo_indptr,
+    const int32_t* __restrict__ kv_indptr, int64_t* __restrict__ positions, int64_t* __restrict__ slot_mapping,
+    int64_t* __restrict__ block_tables, int32_t* __restrict__ block_tables_i32, int32_t* __restrict__ kv_indices) {
   const int s = blockIdx.x;
   const int nc = num_cached[s];
   const int nn = num_new[s];
-  const int tb = table_indptr[s];
-  const int nb = table_indptr[s + 1] - tb;
+  int nb;
+  const int32_t* ids;
+  if (seq_rows) {
+    nb = seq_nblk[s];
+    ids = table_ids + (int64_t)seq_rows[s] * table_stride;
+  } else {
+    const int tb = table_indptr[s];
+    nb = table_indptr[s + 1] - tb;
+    ids = table_ids + tb;
+  }
   const int qs = qo_indptr[s];
   const int ks = kv_indptr[s];
   const int np = kv_indptr[s + 1] - ks;
-  const int32_t* ids = table_ids + tb;
 
   for (int j = threadIdx.x; j < nn; j += blockDim.x) {
     const int p = nc + j;
@@ -107,8 +120,69 @@ __global__ __launch_bounds__(256) void metadata_fill_kernel(
   }
 }
 
+// Resident-mirror updates: entry updates[2 i] of the flat table gets block id updates[2 i + 1].
+__global__ __launch_bounds__(256) void table_update_kernel(int32_t* __restrict__ tables, int64_t table_size,
+                                                           const int32_t* __restrict__ updates, int32_t n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t at = updates[2 * i];
+  if (at >= 0 && at < table_size) tables[at] = updates[2 * i + 1];
+}
+
+int build(const int32_t* num_cached, const int32_t* num_new, const int32_t* table_indptr, const int32_t* table_ids,
+          const int32_t* seq_rows, const int32_t* seq_nblk, int32_t table_stride, int32_t num_seqs,
+          int32_t block_size, int32_t table_width, int64_t* positions, int64_t* slot_mapping, int64_t* block_tables,
+          int64_t* logits_index, int32_t* qo_indptr, int32_t* seq_lens, int32_t* block_tables_i32,
+          int32_t* kv_indptr, int32_t* kv_indices, int32_t* kv_last_page_len, void* stream, const char* fn) {
+  const std::string f = fn;
+  MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, f + ": num_seqs < 0");
+  MLLM_REQUIRE(block_size > 0, MLLM_ERR_INVALID, f + ": block_size must be positive");
+  MLLM_REQUIRE(table_width >= 0, MLLM_ERR_INVALID, f + ": table_width < 0");
+  MLLM_REQUIRE(qo_indptr && kv_indptr, MLLM_ERR_INVALID, f + ": qo_indptr and kv_indptr are required");
+  if (num_seqs > 0) {
+    MLLM_REQUIRE(num_cached && num_new && table_ids && (seq_rows ? seq_nblk != nullptr : table_indptr != nullptr),
+                 MLLM_ERR_INVALID, f + ": null input pointer");
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  metadata_scan_kernel<<<1, kScanThreads, 0, st>>>(num_cached, num_new, num_seqs, block_size, qo_indptr, kv_indptr,
+                                                   seq_lens, kv_last_page_len, logits_index);
+  int rc = check_launch((f + "(scan)").c_str());
+  if (rc) return rc;
+  if (num_seqs == 0) return MLLM_OK;
+  metadata_fill_kernel<<<num_seqs, 256, 0, st>>>(num_cached, num_new, table_indptr, table_ids, seq_rows, seq_nblk,
+                                                  table_stride, block_size, table_width, qo_indptr, kv_indptr,
+                                                  positions, slot_mapping, block_tables, block_tables_i32, kv_indices);
+  return check_launch((f + "(fill)").c_str());
+}
+
 }  // namespace
 }  // namespace mllm
+
+extern "C" int mllm_update_block_tables(int32_t* tables, int64_t table_size, const int32_t* updates,
+                                        int32_t num_updates, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(num_updates >= 0 && table_size >= 0, MLLM_ERR_INVALID, "mllm_update_block_tables: bad sizes");
+  if (num_updates == 0) return MLLM_OK;
+  MLLM_REQUIRE(tables && updates, MLLM_ERR_INVALID, "mllm_update_block_tables: null pointer");
+  table_update_kernel<<<(num_updates + 255) / 256, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      tables, table_size, updates, num_updates);
+  return check_launch("mllm_update_block_tables");
+}
+
+extern "C" int mllm_build_metadata_rows(const int32_t* num_cached, const int32_t* num_new, const int32_t* seq_rows,
+                                        const int32_t* seq_num_blocks, const int32_t* tables, int32_t table_stride,
+                                        int32_t num_seqs, int32_t block_size, int32_t table_width,
+                                        int64_t* positions, int64_t* slot_mapping, int64_t* block_tables,
+                                        int64_t* logits_index, int32_t* qo_indptr, int32_t* seq_lens,
+                                        int32_t* block_tables_i32, int32_t* kv_indptr, int32_t* kv_indices,
+                                        int32_t* kv_last_page_len, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(table_stride > 0, MLLM_ERR_INVALID, "mllm_build_metadata_rows: table_stride must be positive");
+  MLLM_REQUIRE(num_seqs == 0 || seq_rows, MLLM_ERR_INVALID, "mllm_build_metadata_rows: null seq_rows");
+  return build(num_cached, num_new, nullptr, tables, seq_rows, seq_num_blocks, table_stride, num_seqs, block_size,
+               table_width, positions, slot_mapping, block_tables, logits_index, qo_indptr, seq_lens,
+               block_tables_i32, kv_indptr, kv_indices, kv_last_page_len, stream, "mllm_build_metadata_rows");
+}
 
 extern "C" int mllm_build_metadata(const int32_t* num_cached, const int32_t* num_new, const int32_t* table_indptr,
                                    const int32_t* table_ids, int32_t num_seqs, int32_t block_size,
@@ -116,23 +190,7 @@ extern "C" int mllm_build_metadata(const int32_t* num_cached, const int32_t* num
                                    int64_t* block_tables, int64_t* logits_index, int32_t* qo_indptr, int32_t* seq_lens,
                                    int32_t* block_tables_i32, int32_t* kv_indptr, int32_t* kv_indices,
                                    int32_t* kv_last_page_len, void* stream) {
-  using namespace mllm;
-  MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, "mllm_build_metadata: num_seqs < 0");
-  MLLM_REQUIRE(block_size > 0, MLLM_ERR_INVALID, "mllm_build_metadata: block_size must be positive");
-  MLLM_REQUIRE(table_width >= 0, MLLM_ERR_INVALID, "mllm_build_metadata: table_width < 0");
-  MLLM_REQUIRE(qo_indptr && kv_indptr, MLLM_ERR_INVALID, "mllm_build_metadata: qo_indptr and kv_indptr are required");
-  if (num_seqs > 0) {
-    MLLM_REQUIRE(num_cached && num_new && table_indptr && table_ids, MLLM_ERR_INVALID,
-                 "mllm_build_metadata: null input pointer");
-  }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  metadata_scan_kernel<<<1, kScanThreads, 0, st>>>(num_cached, num_new, num_seqs, block_size, qo_indptr, kv_indptr,
-                                                   seq_lens, kv_last_page_len, logits_index);
-  int rc = check_launch("mllm_build_metadata(scan)");
-  if (rc) return rc;
-  if (num_seqs == 0) return MLLM_OK;
-  metadata_fill_kernel<<<num_seqs, 256, 0, st>>>(num_cached, num_new, table_indptr, table_ids, block_size,
-                                                  table_width, qo_indptr, kv_indptr, positions, slot_mapping,
-                                                  block_tables, block_tables_i32, kv_indices);
-  return check_launch("mllm_build_metadata(fill)");
+  return mllm::build(num_cached, num_new, table_indptr, table_ids, nullptr, nullptr, 0, num_seqs, block_size,
+                     table_width, positions, slot_mapping, block_tables, logits_index, qo_indptr, seq_lens,
+                     block_tables_i32, kv_indptr, kv_indices, kv_last_page_len, stream, "mllm_build_metadata");
 }

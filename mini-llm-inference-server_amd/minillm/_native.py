@@ -29,6 +29,9 @@ SIGNATURES = {
     "mllm_last_error": (ctypes.c_char_p, []),
     "mllm_build_metadata": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                            _p]),
+    "mllm_build_metadata_rows": (ctypes.c_int, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p,
+                                                _p, _p, _p, _p, _p]),
+    "mllm_update_block_tables": (ctypes.c_int, [_p, _i64, _p, _i32, _p]),
     "mllm_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _i32, _i64, _i32, _i32, _p, _i64,
                                       _p]),
     "mllm_rope_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32, _i32,

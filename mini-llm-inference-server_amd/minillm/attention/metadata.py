@@ -123,6 +123,18 @@ class AttentionMetadata:
                    block_tables_i32=tables_i32, kv_indptr=kv_indptr, kv_indices=kv_indices,
                    kv_last_page_len=last_len)
 
+    def _launch_build_rows(self, packed: torch.Tensor, tables: DeviceBlockTables, width: int) -> None:
+        """mllm_build_metadata_rows from num_cached | num_new | rows | num_blocks at the front of `packed`."""
+        n_seq = self.num_seqs
+        base = packed.data_ptr()
+        _native.lib().call(
+            "mllm_build_metadata_rows", base, base + 4 * n_seq, base + 8 * n_seq, base + 12 * n_seq,
+            tables.tables.data_ptr(), tables.max_blocks, n_seq, self.block_size, width, self.positions.data_ptr(),
+            self.slot_mapping.data_ptr(), self.block_tables.data_ptr(), self.logits_index.data_ptr(),
+            self.qo_indptr.data_ptr(), self.seq_lens_i32.data_ptr(), self.block_tables_i32.data_ptr(),
+            self.kv_indptr.data_ptr(), self.kv_indices.data_ptr(), self.kv_last_page_len.data_ptr(),
+            _native.stream_ptr(packed.device))
+
     def _launch_build(self, packed: torch.Tensor, width: int) -> None:
         """mllm_build_metadata from a packed device upload (see pack_steps) into this object's arenas."""
         n_seq = self.num_seqs
@@ -133,6 +145,89 @@ class AttentionMetadata:
             self.block_tables.data_ptr(), self.logits_index.data_ptr(), self.qo_indptr.data_ptr(),
             self.seq_lens_i32.data_ptr(), self.block_tables_i32.data_ptr(), self.kv_indptr.data_ptr(),
             self.kv_indices.data_ptr(), self.kv_last_page_len.data_ptr(), _native.stream_ptr(packed.device))
+
+
+class DeviceBlockTables:
+    """A device-resident mirror of the block manager's tables: one row of `max_blocks` int32 block ids per
+    request (keyed by any hashable, the engine's Request objects), so a step uploads only the ids each
+    request gained since its last step instead of every table (the reference's build flattens and uploads
+    all of them, metadata.py:82-83,101).  A request's list of block ids only grows while it runs; a new
+    list object (re-admission after preemption) is uploaded whole.  Row `max_rows` is reserved for
+    padding rows: its only block id is -1."""
+
+    def __init__(self, max_rows: int, max_blocks: int, device) -> None:
+        self.max_rows, self.max_blocks = int(max_rows), int(max_blocks)
+        self.device = torch.device(device)
+        self.pad_row = self.max_rows
+        self.tables = torch.zeros((self.max_rows + 1) * self.max_blocks, dtype=torch.int32, device=self.device)
+        self.tables[self.pad_row * self.max_blocks] = -1
+        self._free = list(range(self.max_rows - 1, -1, -1))
+        self._row: dict = {}
+        self._synced: dict = {}  # key -> (the block-id list object, entries already on the device)
+
+    def release(self, key) -> None:
+        row = self._row.pop(key, None)
+        if row is not None:
+            self._free.append(row)
+            self._synced.pop(key, None)
+
+    def sync(self, keys, seqs: list[SeqStep]) -> tuple[list[int], list[int]]:
+        """Rows of the step's sequences and the flat (index, id) updates that bring them up to date."""
+        rows, updates = [], []
+        for key, s in zip(keys, seqs):
+            ids = s.block_ids
+            if len(ids) > self.max_blocks:
+                raise ValueError(f"{len(ids)} blocks exceed the resident table's {self.max_blocks} per row")
+            row = self._row.get(key)
+            if row is None:
+                if not self._free:
+                    raise ValueError(f"more than {self.max_rows} requests hold resident table rows")
+                row = self._row[key] = self._free.pop()
+            prev = self._synced.get(key)
+            start = prev[1] if prev is not None and prev[0] is ids and prev[1] <= len(ids) else 0
+            base = row * self.max_blocks
+            for j in range(start, len(ids)):
+                updates += (base + j, ids[j])
+            self._synced[key] = (ids, len(ids))
+            rows.append(row)
+        return rows, updates
+
+    def build(self, keys, seqs: list[SeqStep], block_size: int) -> AttentionMetadata:
+        """AttentionMetadata of a step (same fields, bit-identical) from the resident tables: one upload of
+        num_cached | num_new | rows | num_blocks | updates, a table update and the two build launches."""
+        if not seqs:
+            raise ValueError("a step needs at least one sequence")
+        bs = int(block_size)
+        starts, lens = [0], []
+        for s in seqs:
+            end = s.num_cached + s.num_new
+            if len(s.block_ids) * bs < end:
+                raise ValueError(f"{len(s.block_ids)} blocks can't hold {end} tokens")
+            starts.append(starts[-1] + s.num_new)
+            lens.append(end)
+        rows, updates = self.sync(keys, seqs)
+        n_seq = len(seqs)
+        nblk = [len(s.block_ids) for s in seqs]
+        host = np.empty(4 * n_seq + len(updates), dtype=np.int32)
+        host[:n_seq] = [s.num_cached for s in seqs]
+        host[n_seq:2 * n_seq] = [s.num_new for s in seqs]
+        host[2 * n_seq:3 * n_seq] = rows
+        host[3 * n_seq:4 * n_seq] = nblk
+        host[4 * n_seq:] = updates
+        packed = torch.from_numpy(host).to(self.device)
+        width = max(nblk)
+        meta = AttentionMetadata._arenas(bs, starts, lens, starts[-1], width, sum(-(-n // bs) for n in lens),
+                                         self.device)
+        self.apply(packed, 4 * n_seq, len(updates) // 2)
+        meta._launch_build_rows(packed, self, width)
+        meta._upload = packed
+        return meta
+
+    def apply(self, packed: torch.Tensor, offset: int, num_updates: int) -> None:
+        """mllm_update_block_tables from `num_updates` (index, id) pairs at int32 offset `offset` of `packed`."""
+        if num_updates:
+            _native.lib().call("mllm_update_block_tables", self.tables.data_ptr(), self.tables.numel(),
+                               packed.data_ptr() + 4 * offset, num_updates, _native.stream_ptr(self.device))
 
 
 def pack_steps(seqs: list[SeqStep], out: np.ndarray) -> np.ndarray:
@@ -152,35 +247,39 @@ def pack_steps(seqs: list[SeqStep], out: np.ndarray) -> np.ndarray:
 
 class StaticDecodeMetadata:
     """Metadata of a decode step of exactly `num_rows` rows (one new token each) in fixed device buffers,
-    for HIP graph capture: the arenas, the packed upload buffer and its pinned host twin never move, so
-    a captured `build()` reads whatever `load()` last put there.
+    for HIP graph capture: the arenas, the upload buffer and its pinned host twin never move, and the
+    block ids come from a DeviceBlockTables mirror, so a captured `build()` reads whatever `load()` last
+    staged.
 
-    Rows past the step's own are padding: one cached-less token whose only block id is -1, so its slot is
-    negative (the append skips it) and its page reads are clamped inside the pool.  The host lists hold
-    the worst case (every row at `max_blocks` blocks), which is what a plan built from them must cover.
-    The step's split-KV size is staged too (`meta.split_dev`, at least `meta.split_min` pages), so the
-    captured plan splits each replayed step as an eager step of the same rows would."""
+    Rows past the step's own are padding: a cached-less token on the mirror's pad row (block id -1), so its
+    slot is negative (the append skips it) and its page reads are clamped inside the pool.  The host lists
+    hold the worst case (every row at the mirror's `max_blocks` blocks), which is what a plan built from
+    them must cover.  The step's split-KV size is staged too (`meta.split_dev`, at least `meta.split_min`
+    pages), so the captured plan splits each replayed step as an eager step of the same rows would."""
 
     SPLIT_MIN = 8  # the smallest split the host heuristic picks: the plan's capacities are sized for it
 
-    def __init__(self, num_rows: int, max_blocks: int, block_size: int, device) -> None:
-        self.num_rows, self.max_blocks, self.block_size = num_rows, max_blocks, block_size
-        cap = 3 * num_rows + 1 + num_rows * max_blocks
-        self.pinned = torch.empty(cap + 1, dtype=torch.int32, pin_memory=True)  # + the split size
-        self.packed = torch.zeros(cap + 1, dtype=torch.int32, device=device)
+    def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int) -> None:
+        self.num_rows, self.tables, self.block_size = num_rows, tables, block_size
+        self.max_blocks = tables.max_blocks
+        dev = tables.device
+        # num_cached | num_new | rows | num_blocks | split size | table updates (at most every entry of B rows)
+        self._upd = 4 * num_rows + 1
+        cap = self._upd + 2 * num_rows * self.max_blocks
+        self.pinned = torch.empty(cap, dtype=torch.int32, pin_memory=True)
+        self.packed = torch.zeros(cap, dtype=torch.int32, device=dev)
         self.meta = AttentionMetadata._arenas(block_size, list(range(num_rows + 1)),
-                                              [max_blocks * block_size] * num_rows, num_rows, max_blocks,
-                                              num_rows * max_blocks, device)
-        self.meta.split_dev = self.packed[cap:]
+                                              [self.max_blocks * block_size] * num_rows, num_rows, self.max_blocks,
+                                              num_rows * self.max_blocks, dev)
+        self.meta.split_dev = self.packed[4 * num_rows:4 * num_rows + 1]
         self.meta.split_min = self.SPLIT_MIN
-        self._cap = cap
-        self._pad = SeqStep(0, 1, [-1])
 
-    def load(self, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
-        """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host
-        packing plus one non-blocking copy on the current stream."""
-        if len(seqs) > self.num_rows:
-            raise ValueError(f"{len(seqs)} rows do not fit a {self.num_rows}-row decode graph")
+    def load(self, keys, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
+        """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host packing,
+        one non-blocking copy and the mirror's update launch, on the current stream."""
+        b = self.num_rows
+        if len(seqs) > b:
+            raise ValueError(f"{len(seqs)} rows do not fit a {b}-row decode graph")
         bs = self.block_size
         for s in seqs:
             if s.num_new != 1:
@@ -188,16 +287,26 @@ class StaticDecodeMetadata:
             end = s.num_cached + 1
             if len(s.block_ids) * bs < end:
                 raise ValueError(f"{len(s.block_ids)} blocks can't hold {end} tokens")
-            if -(-end // bs) > self.max_blocks:
-                raise ValueError(f"a row of {end} tokens exceeds the graph's {self.max_blocks} blocks")
-        rows = [SeqStep(s.num_cached, 1, s.block_ids[:-(-(s.num_cached + 1) // bs)]) for s in seqs]
-        rows += [self._pad] * (self.num_rows - len(seqs))
+            if len(s.block_ids) > self.max_blocks:
+                raise ValueError(f"a row of {len(s.block_ids)} blocks exceeds the graph's {self.max_blocks} blocks")
+        rows, updates = self.tables.sync(keys, seqs)
+        n, pad = len(seqs), b - len(seqs)
         host = self.pinned.numpy()
-        n = len(pack_steps(rows, host))
-        host[self._cap] = max(self.SPLIT_MIN, min(128, int(pages_per_split)))
-        self.packed[:n].copy_(self.pinned[:n], non_blocking=True)
-        self.packed[self._cap:].copy_(self.pinned[self._cap:], non_blocking=True)
+        host[:n] = [s.num_cached for s in seqs]
+        host[n:b] = 0
+        host[b:2 * b] = 1
+        host[2 * b:2 * b + n] = rows
+        host[2 * b + n:3 * b] = self.tables.pad_row
+        host[3 * b:3 * b + n] = [len(s.block_ids) for s in seqs]
+        host[3 * b + n:4 * b] = 1
+        host[4 * b] = max(self.SPLIT_MIN, min(128, int(pages_per_split)))
+        u = len(updates)
+        host[self._upd:self._upd + u] = updates
+        end = self._upd + u
+        self.packed[:end].copy_(self.pinned[:end], non_blocking=True)
+        self.tables.apply(self.packed, self._upd, u // 2)
+        del pad
 
     def build(self) -> None:
-        """mllm_build_metadata over the staged step (capturable: fixed pointers and launch shapes)."""
-        self.meta._launch_build(self.packed, self.max_blocks)
+        """mllm_build_metadata_rows over the staged step (capturable: fixed pointers and launch shapes)."""
+        self.meta._launch_build_rows(self.packed, self.tables, self.max_blocks)

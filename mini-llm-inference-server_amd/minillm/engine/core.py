@@ -13,7 +13,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from ..attention.metadata import AttentionMetadata, SeqStep
+from ..attention.metadata import AttentionMetadata, DeviceBlockTables, SeqStep
 from ..cache.paged import BLOCK_SIZE, PagedKVCache
 from ..cache.prefix import PrefixCache, root_hash
 from .block_manager import BlockManager
@@ -88,15 +88,17 @@ class EngineCore:
                  enable_prefix_caching: bool = True, model_id: str = "unknown", metadata_builder=None,
                  chunked_prefill: bool = False, kv_cache_dtype: torch.dtype | None = None,
                  kv_scales: tuple[float, float] = (1.0, 1.0), decode_graphs=None) -> None:
-        """`metadata_builder(seqs, block_size, device)` defaults to AttentionMetadata.build (the GPU
-        build); a test may pass another implementation of the same contract.  `chunked_prefill` mixes
+        """The step's metadata comes from a device-resident mirror of the block tables (DeviceBlockTables:
+        only new block ids travel each step); `metadata_builder(seqs, block_size, device)` replaces that with
+        another implementation of the same contract (AttentionMetadata.build uploads every table; a test
+        passes the oracle's).  `chunked_prefill` mixes
         decode rows and prompt chunks in one step under the token budget (see Scheduler).
         `kv_cache_dtype` defaults to the model's dtype; torch.float8_e4m3fn gives an fp8 pool whose K and
         V tensors of every layer use the per-tensor scales `kv_scales` (k_scale, v_scale).
         `decode_graphs` (True, or a tuple of batch buckets) runs pure decode steps as captured HIP graphs
         (DecodeGraphs); prefill and mixed steps stay eager."""
         self.model = model
-        self.build_metadata = metadata_builder or AttentionMetadata.build
+        self.build_metadata = metadata_builder
         p = next(model.parameters())
         self.device, self.dtype = p.device, p.dtype
         self.max_model_len = max_model_len or model.config.max_position_embeddings
@@ -114,12 +116,17 @@ class EngineCore:
                            "layout": "NHD", "model": model_id}
         if self.cache.quantized:  # the stored bytes depend on the scales too
             self._salt_keys["kv_scales"] = [kv_scales[0], kv_scales[1]]
+        self.tables = None
+        if metadata_builder is None:
+            self.tables = DeviceBlockTables(max_batch_size, -(-self.max_model_len // BLOCK_SIZE), self.device)
         self.graphs = None
         if decode_graphs:
             from .graphs import DEFAULT_BUCKETS, DecodeGraphs
 
+            if self.tables is None:
+                raise ValueError("decode graphs read the resident block tables: leave metadata_builder unset")
             buckets = DEFAULT_BUCKETS if decode_graphs is True else tuple(decode_graphs)
-            self.graphs = DecodeGraphs(model, self.cache, self.max_model_len, BLOCK_SIZE, buckets)
+            self.graphs = DecodeGraphs(model, self.cache, self.tables, BLOCK_SIZE, buckets)
         self.step_log: list[StepRecord] | None = [] if step_log else None
         self._step = 0
         self._aborted: list[RequestOutput] = []
@@ -143,6 +150,7 @@ class EngineCore:
         req = next((r for r in self.scheduler.running if r.req_id == req_id), None)
         if req is not None:
             self.scheduler.finish([req])
+            self._release(req)
         else:
             req = self.scheduler.remove_waiting(req_id)
             if req is None:
@@ -171,6 +179,8 @@ class EngineCore:
         outputs, self._aborted = self._aborted, []
         t0 = now_ns()
         plan = self.scheduler.schedule()
+        for r in plan.preempted:
+            self._release(r)
         rows = plan.rows()
         if not rows:
             return StepOutputs(outputs, self.stats())
@@ -180,9 +190,12 @@ class EngineCore:
         new = [r.uncached()[:n] for r, n in rows]
         seqs = [SeqStep(r.num_cached, len(n), r.block_ids) for r, n in zip(reqs, new)]
         if self.graphs is not None and not plan.prefill and self.graphs.supports(len(seqs)):
-            tokens = self.graphs.run(seqs, [n[0] for n in new])
+            tokens = self.graphs.run(reqs, seqs, [n[0] for n in new])
         else:
-            meta = self.build_metadata(seqs, BLOCK_SIZE, self.device)
+            if self.tables is not None:
+                meta = self.tables.build(reqs, seqs, BLOCK_SIZE)
+            else:
+                meta = self.build_metadata(seqs, BLOCK_SIZE, self.device)
             ids = torch.tensor([[t for n in new for t in n]], device=self.device)
             logits = self.model(ids, kv_cache=self.cache.step(meta), last_index=meta.logits_index)
             tokens = logits[:, -1].argmax(dim=-1).tolist()
@@ -202,6 +215,8 @@ class EngineCore:
                 outputs.append(RequestOutput(req.req_id, [token]))
         self.scheduler.name_full_blocks(reqs)
         self.scheduler.finish(done)
+        for r in done:
+            self._release(r)
         if self.step_log is not None:
             st = self.stats()
             self.step_log.append(StepRecord(self._step, t0, now_ns() - t0, len(reqs),
@@ -210,6 +225,11 @@ class EngineCore:
                                             len(plan.preempted)))
         self._step += 1
         return StepOutputs(outputs, self.stats())
+
+    def _release(self, req: Request) -> None:
+        """The request left the running set: its resident table row is free again."""
+        if self.tables is not None:
+            self.tables.release(req)
 
     def _finish(self, req: Request, new_tokens: list[int], reason: str) -> RequestOutput:
         req.timeline["finished"] = now_ns()

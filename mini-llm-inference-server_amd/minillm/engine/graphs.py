@@ -25,7 +25,7 @@ from __future__ import annotations
 import torch
 
 from ..attention.hip_backend import pages_per_split
-from ..attention.metadata import SeqStep, StaticDecodeMetadata
+from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
 
@@ -42,13 +42,12 @@ class _Captured:
 class DecodeGraphs:
     """Captured decode steps of `model` over `cache`, one graph per bucket, captured on first use."""
 
-    def __init__(self, model, cache, max_model_len: int, block_size: int, buckets=DEFAULT_BUCKETS) -> None:
+    def __init__(self, model, cache, tables: DeviceBlockTables, block_size: int, buckets=DEFAULT_BUCKETS) -> None:
         backend = model.model.layers[0].self_attn.backend
         if not hasattr(backend, "invalidate_plan"):
             raise ValueError("decode graphs need the hip attention backend")
-        self.model, self.cache, self.backend = model, cache, backend
+        self.model, self.cache, self.backend, self.tables = model, cache, backend, tables
         self.block_size = block_size
-        self.max_blocks = -(-max_model_len // block_size)
         self.buckets = tuple(sorted(set(int(b) for b in buckets)))
         self.device = next(model.parameters()).device
         self.num_kv_heads = model.config.num_key_value_heads
@@ -63,12 +62,12 @@ class DecodeGraphs:
     def bucket(self, num_rows: int) -> int:
         return next(b for b in self.buckets if b >= num_rows)
 
-    def run(self, seqs: list[SeqStep], token_ids: list[int]) -> list[int]:
-        """One decode step: `seqs` are the rows (one new token each, its id in `token_ids`).  Returns each
-        row's greedy next token."""
+    def run(self, keys, seqs: list[SeqStep], token_ids: list[int]) -> list[int]:
+        """One decode step: `seqs` are the rows (one new token each, its id in `token_ids`), `keys` their
+        requests' keys in the resident tables.  Returns each row's greedy next token."""
         b = self.bucket(len(seqs))
         c = self.captured(b)
-        self._stage(c, seqs, token_ids)
+        self._stage(c, keys, seqs, token_ids)
         c.graph.replay()
         self.replays += 1
         self.last_bucket = b
@@ -81,10 +80,10 @@ class DecodeGraphs:
 
     # ------------------------------------------------------------------ internals
 
-    def _stage(self, c: _Captured, seqs: list[SeqStep], token_ids: list[int]) -> None:
+    def _stage(self, c: _Captured, keys, seqs: list[SeqStep], token_ids: list[int]) -> None:
         bs = self.block_size
         pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs)
-        c.static.load(seqs, pages_per_split(pages, self.num_kv_heads))  # the eager step's split size
+        c.static.load(keys, seqs, pages_per_split(pages, self.num_kv_heads))  # the eager step's split size
         ids = c.pinned_ids.numpy()
         ids[:len(token_ids)] = token_ids
         ids[len(token_ids):] = 0
@@ -100,10 +99,10 @@ class DecodeGraphs:
 
     @torch.inference_mode()
     def _capture(self, bucket: int) -> _Captured:
-        static = StaticDecodeMetadata(bucket, self.max_blocks, self.block_size, self.device)
+        static = StaticDecodeMetadata(bucket, self.tables, self.block_size)
         c = _Captured(static, torch.zeros((1, bucket), dtype=torch.long, device=self.device),
                       torch.zeros(bucket, dtype=torch.long, pin_memory=True))
-        self._stage(c, [], [])  # every row padding: a valid step that writes nothing to the pool
+        self._stage(c, [], [], [])  # every row padding: a valid step that writes nothing to the pool
         # warm-up on a side stream (sizes a fresh workspace for the worst-case plan), then capture
         self.backend.detach_workspace()
         side = torch.cuda.Stream(self.device)

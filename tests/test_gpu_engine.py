@@ -87,10 +87,12 @@ def test_engine_greedy_tokens_match_oracle(hip):
     model = tiny_model()
     ps = prompts(12, 1, 300, seed=1)
     kw = dict(max_batch_size=8, num_kv_blocks=400, max_model_len=4096)
-    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 24, **kw)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 24, **kw)  # resident block tables
     exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 24, **kw)
     assert_greedy_match(got, exp)
-    assert core.stats().num_running == 0
+    assert core.stats().num_running == 0 and core.tables is not None
+    csr, _ = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 24, **kw)  # tables uploaded whole
+    assert csr == got
 
 
 def test_engine_with_preemption_and_prefix_sharing(hip):
@@ -102,7 +104,7 @@ def test_engine_with_preemption_and_prefix_sharing(hip):
     head = prompts(1, 48, 49, seed=5)[0]
     ps = [head + p for p in prompts(6, 5, 40, seed=6)]
     kw = dict(max_batch_size=6, num_kv_blocks=24, max_model_len=4096)
-    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 40, **kw)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 40, **kw)
     exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 40, **kw)
     assert_greedy_match(got, exp)
     st = core.stats()
@@ -167,7 +169,7 @@ def test_chunked_prefill_engine_matches_oracle(hip):
 
     model = tiny_model(seed=13)
     ps = prompts(10, 1, 400, seed=14)
-    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, max_batch_size=8,
+    got, core = run_engine(model, get_backend("hip"), None, ps, 20, max_batch_size=8,
                            num_kv_blocks=400, max_model_len=4096, chunked_prefill=True, max_num_batched_tokens=96,
                            step_log=True)
     exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 20, max_batch_size=8, num_kv_blocks=400,
@@ -188,7 +190,7 @@ def test_fp8_pool_engine_matches_oracle(hip):
     ps = [head + p for p in prompts(8, 1, 300, seed=23)]
     kw = dict(max_batch_size=6, num_kv_blocks=64, max_model_len=4096, kv_cache_dtype=torch.float8_e4m3fn,
               kv_scales=(0.5, 0.25))
-    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 24, **kw)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 24, **kw)
     exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 24, **kw)
     assert_greedy_match(got, exp)
     assert core.cache.k[0].dtype == torch.float8_e4m3fn

@@ -54,19 +54,19 @@ def test_graph_engine_matches_eager_engine(hip, kv):
     kw = dict(max_batch_size=8, num_kv_blocks=300, max_model_len=2048)
     if kv == "fp8":
         kw.update(kv_cache_dtype=torch.float8_e4m3fn, kv_scales=(0.5, 0.25))
-    got, core = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, decode_graphs=True, **kw)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 20, decode_graphs=True, **kw)
     exp, _ = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 20, **kw)
     assert_greedy_match(got, exp)
     assert core.graphs.replays > 10 and len(core.graphs._captured) >= 2  # batch shrinks as requests finish
 
 
 def test_graph_rejects_what_it_cannot_hold(hip):
-    from minillm.attention.metadata import SeqStep, StaticDecodeMetadata
+    from minillm.attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata
 
-    sm = StaticDecodeMetadata(4, 8, 16, DEV)
+    sm = StaticDecodeMetadata(4, DeviceBlockTables(8, 8, DEV), 16)
     with pytest.raises(ValueError, match="decode graph"):
-        sm.load([SeqStep(0, 1, [1])] * 5)
+        sm.load(list(range(5)), [SeqStep(0, 1, [1])] * 5)
     with pytest.raises(ValueError, match="one new token"):
-        sm.load([SeqStep(0, 2, [1])])
+        sm.load([0], [SeqStep(0, 2, [1])])
     with pytest.raises(ValueError, match="exceeds"):
-        sm.load([SeqStep(200, 1, list(range(13)))])
+        sm.load([0], [SeqStep(200, 1, list(range(13)))])

@@ -70,6 +70,50 @@ def test_metadata_random_steps(hip, bs, seed):
     _meta_fields_equal(meta, build_metadata([OracleSeq(*s) for s in seqs], bs))
 
 
+@pytest.mark.parametrize("bs", [4, 16])
+def test_metadata_from_resident_tables(hip, bs):
+    # the device mirror across 40 steps of a churning request set: tables grow by appends, some requests
+    # leave (rows released and reused), some come back with a new list; every step's fields equal the
+    # oracle's build from the full tables, bit for bit, and the KAT holds on a fresh mirror
+    from minillm.attention.metadata import DeviceBlockTables, SeqStep
+
+    g = json.loads((GOLDEN / "metadata_kat.json").read_text())
+    kat = DeviceBlockTables(4, 8, DEV).build(["x", "y"], [SeqStep(c, n, b) for c, n, b in g["seqs"]],
+                                             g["block_size"])
+    for name, exp in g["expected"].items():
+        got = getattr(kat, name)
+        assert (got if isinstance(got, list) else got.cpu().tolist()) == exp, name
+
+    rng = random.Random(bs)
+    tables = DeviceBlockTables(64, 6000 // bs + 16, DEV)  # rows reach 1000 + 40 x 100 tokens at most
+    live: dict[int, list] = {}  # key -> [num_cached, block_ids]
+    next_block, next_key = 0, 0
+    for step in range(40):
+        for key in [k for k in live if rng.random() < 0.1]:  # finished, or preempted and requeued
+            tables.release(key)
+            if rng.random() < 0.5:
+                live[key] = [0, []]  # back later under the same key with a new list, recomputed from 0
+            else:
+                del live[key]
+        while len(live) < 40 and rng.random() < 0.7:  # admitted, some with a long cached prefix
+            cached = rng.choice([0, rng.randrange(0, 1000)])
+            live[next_key] = [cached, []]
+            next_key += 1
+        keys = [k for k in live if rng.random() < 0.9] or list(live)[:1]
+        seqs = []
+        for k in keys:
+            cached, ids = live[k]
+            new = rng.choice([1, 1, 1, rng.randrange(1, 100)])
+            while len(ids) * bs < cached + new:
+                ids.append(next_block % 5000)  # in-place appends: only these travel
+                next_block += 7
+            seqs.append(SeqStep(cached, new, ids))
+            live[k][0] = cached + new
+        meta = tables.build(keys, seqs, bs)
+        _meta_fields_equal(meta, build_metadata([OracleSeq(s.num_cached, s.num_new, list(s.block_ids))
+                                                 for s in seqs], bs))
+
+
 @pytest.mark.parametrize("name", ["decode_4", "decode_256", "mixed_128", "prefix_64"])
 def test_metadata_workloads(hip, name):
     from minillm import workloads

@@ -125,3 +125,28 @@ def test_packed_step_upload_layout():
     got = pack_steps([SeqStep(3, 1, [7]), SeqStep(0, 5, [2, 9])], out)
     assert got.tolist() == [3, 0, 1, 5, 0, 1, 3, 7, 2, 9]
     assert out[10:].tolist() == [99] * 6  # nothing written past the packed step
+
+
+def test_resident_tables_send_only_new_block_ids():
+    # the host side of the device mirror: rows per request, and per step only the ids a request gained
+    from minillm.attention.metadata import DeviceBlockTables, SeqStep
+
+    t = DeviceBlockTables(max_rows=3, max_blocks=4, device="cpu")
+    assert t.tables[t.pad_row * 4].item() == -1
+    a_ids, b_ids = [5, 6], [9]
+    rows, upd = t.sync(["a", "b"], [SeqStep(20, 1, a_ids), SeqStep(0, 3, b_ids)])
+    ra, rb = rows
+    assert upd == [ra * 4, 5, ra * 4 + 1, 6, rb * 4, 9]
+    a_ids += [7]  # a crosses a block boundary: only the new id travels
+    rows2, upd2 = t.sync(["a", "b"], [SeqStep(32, 1, a_ids), SeqStep(3, 1, b_ids)])
+    assert rows2 == rows and upd2 == [ra * 4 + 2, 7]
+    rows3, upd3 = t.sync(["a"], [SeqStep(0, 5, [1, 2])])  # a new list object (re-admission): uploaded whole
+    assert rows3 == [ra] and upd3 == [ra * 4, 1, ra * 4 + 1, 2]
+    t.release("b")
+    rows4, _ = t.sync(["c"], [SeqStep(0, 1, [3])])
+    assert rows4 == [rb]  # the freed row is reused
+    with pytest.raises(ValueError, match="exceed"):
+        t.sync(["d"], [SeqStep(0, 1, [1, 2, 3, 4, 5])])
+    t.sync(["d"], [SeqStep(0, 1, [1])])
+    with pytest.raises(ValueError, match="more than 3 requests"):
+        t.sync(["e"], [SeqStep(0, 1, [1])])
