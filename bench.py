@@ -257,7 +257,7 @@ def main():
 
     from minillm import workloads
     from minillm.attention.hip_backend import HipBackend
-    from minillm.attention.metadata import AttentionMetadata, SeqStep
+    from minillm.attention.metadata import AttentionMetadata, DeviceBlockTables, SeqStep
 
     if args.workload == "engine_8b":
         return bench_engine(args)
@@ -275,7 +275,9 @@ def main():
     seqs = [SeqStep(c, n, b) for c, n, b in wl.seqs]
     backend = HipBackend()
 
-    # per-step costs shared by the 32 layers: metadata build (host + GPU) and the GPU work plan
+    # per-step costs shared by the 32 layers: metadata build (host + GPU) and the GPU work plan, with every
+    # table uploaded (AttentionMetadata.build) and from the engine's resident tables in steady state (a
+    # step that allocated no new block: only num_cached, num_new and row ids travel)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(5):
@@ -284,6 +286,20 @@ def main():
         backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
     torch.cuda.synchronize()
     meta_plan_ms = (time.perf_counter() - t0) / 5 * 1e3
+    tables = DeviceBlockTables(len(seqs), max(len(s.block_ids) for s in seqs), dev)
+    keys = list(range(len(seqs)))
+    tables.build(keys, seqs, wl.block_size)  # the first step uploads every table
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        rmeta = tables.build(keys, seqs, wl.block_size)
+        backend._planned = None
+        backend.plan(rmeta, wl.h, wl.hkv, wl.dh, dev)
+    torch.cuda.synchronize()
+    resident_ms = (time.perf_counter() - t0) / 5 * 1e3
+    del rmeta
+    backend._planned = None
+    backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
 
     out = torch.empty_like(q)
     plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
@@ -370,9 +386,28 @@ def main():
                       "hbm_frac": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                       "decode_us": round(dec_ms * 1e3, 2), "prefill_us": round(pf_ms * 1e3, 2),
                       "prefill_tflops": round(wl.prefill_flops() / (pf_ms * 1e-3) / 1e12, 1) if pf_ms else None},
-        "per_step_shared_ms": {"metadata_build_and_plan": round(meta_plan_ms, 3)},
+        "per_step_shared_ms": {"metadata_build_and_plan": round(meta_plan_ms, 3),
+                               "resident_tables_build_and_plan": round(resident_ms, 3)},
         "wall_ms_timed_region": round(wall_ms, 2),
     }
+    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step: prefill beside decode
+        def ostep():
+            backend.append(k, v, pool_k, pool_v, meta, ks, vs)
+            backend.attend(q, pool_k, pool_v, meta, out, ks, vs)
+
+        for _ in range(3):
+            ostep()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            ostep()
+        b.record()
+        torch.cuda.synchronize()
+        o_ms = a.elapsed_time(b) / args.steps
+        line["mixed_overlap"] = {"step_us": round(o_ms * 1e3, 2), "sequential_step_us": round(step_ms * 1e3, 2),
+                                 "tokens_per_s": round(wl.num_tokens / (LAYERS * o_ms * 1e-3), 1),
+                                 "note": "append, then the prefill launch on a second stream beside decode + merge"}
     line["rotary_append"] = rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v)
     if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_rows)

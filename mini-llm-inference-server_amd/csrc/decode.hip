@@ -310,11 +310,16 @@ constexpr int kOccupancy = 3;
 #define MLLM_DECODE_FP8_PREFETCH 2
 #endif
 constexpr int kPrefetchFp8 = MLLM_DECODE_FP8_PREFETCH;
+#ifndef MLLM_DECODE_FP8_OCC
+#define MLLM_DECODE_FP8_OCC 3
+#endif
+constexpr int kOccupancyFp8 = MLLM_DECODE_FP8_OCC;
 
 template <typename T, bool F8>
 int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
   const unsigned grid = (unsigned)n_work * (unsigned)a.HG;
-  decode_kernel<T, F8, F8 ? kPrefetchFp8 : kPrefetch, kNonTemporal, kOccupancy><<<grid, 64 * kWaves, 0, st>>>(a);
+  decode_kernel<T, F8, F8 ? kPrefetchFp8 : kPrefetch, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy>
+      <<<grid, 64 * kWaves, 0, st>>>(a);
   return check_launch(F8 ? "mllm_paged_decode_fp8" : "mllm_paged_decode");
 }
 

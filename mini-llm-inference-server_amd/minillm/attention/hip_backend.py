@@ -73,12 +73,16 @@ class HipBackend(AttentionBackend):
     # The model hands q and k to `forward_rotary` before RoPE when this is set (LlamaAttention checks it),
     # so the rotation runs in the KV-append launch; False gives the reference call sequence.
     fuse_rotary = True
+    # A step with decode rows and multi-token rows runs the prefill launch on a second stream beside the
+    # decode launch (HBM-bound and MFMA-bound work overlap); their outputs are disjoint rows of `out`.
+    overlap_mixed = True
 
     def __init__(self) -> None:
         self._lib = _native.lib()
         self._planned = None  # the AttentionMetadata the plan was last built for
         self._plan: StepPlan | None = None
         self._workspace: torch.Tensor | None = None
+        self._side: dict = {}  # device -> the stream mixed steps run their prefill launch on
 
     # ------------------------------------------------------------------ paged path
 
@@ -184,6 +188,18 @@ class HipBackend(AttentionBackend):
     def attend(self, q, k_cache, v_cache, meta, out, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """Attention of every new token over its row's context in the pool, written into `out`."""
         plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device)
+        if plan.num_decode and plan.num_prefill and self.overlap_mixed and not torch.cuda.is_current_stream_capturing():
+            cur = torch.cuda.current_stream(q.device)
+            side = self._side.get(q.device)
+            if side is None:
+                side = self._side[q.device] = torch.cuda.Stream(q.device)  # default priority
+            side.wait_stream(cur)  # the append (and everything before it) has landed
+            with torch.cuda.stream(side):
+                self.run_prefill(q, k_cache, v_cache, meta, out, k_scale, v_scale)
+            self.run_decode(q, k_cache, v_cache, meta, out, k_scale, v_scale)
+            self.run_merge(q, meta, out)
+            cur.wait_stream(side)  # nothing after attend runs before the prefill rows are written
+            return
         if plan.num_decode:
             self.run_decode(q, k_cache, v_cache, meta, out, k_scale, v_scale)
             self.run_merge(q, meta, out)

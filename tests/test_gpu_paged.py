@@ -139,6 +139,21 @@ def test_workload_parity(hip, name):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+def test_mixed_step_overlap_is_bit_identical(hip):
+    # the prefill launch on a second stream beside decode + merge gives the sequential step's output
+    from minillm import workloads
+    from minillm.attention.hip_backend import HipBackend
+
+    wl = workloads.mixed_128()
+    outs = []
+    for overlap in (False, True):
+        be = HipBackend()
+        be.overlap_mixed = overlap
+        outs.append(hip_step(wl, DEV, backend=be)[0])
+    torch.cuda.synchronize()
+    assert torch.equal(bits(outs[0]), bits(outs[1]))
+
+
 def test_fp16_pool_parity(hip):
     from minillm import workloads
 
