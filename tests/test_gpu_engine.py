@@ -196,3 +196,20 @@ def test_fp8_pool_engine_matches_oracle(hip):
     assert core.cache.k[0].dtype == torch.float8_e4m3fn
     st = core.stats()
     assert st.num_preemptions > 0 and st.prefix_cache_hits > 0
+
+
+def test_prefix_cache_changes_no_token(hip):
+    # reference tests/test_prefix_cache.py:112-209: shared prompt heads served from cached pages give the
+    # tokens of a run without the cache, also when a small pool evicts cached blocks LRU
+    from minillm.attention import get_backend
+
+    model = tiny_model(seed=51)
+    heads = prompts(3, 48, 49, seed=52)
+    ps = [heads[i % 3] + p for i, p in enumerate(prompts(9, 1, 60, seed=53))]
+    kw = dict(max_batch_size=3, max_model_len=4096)
+    off, _ = run_engine(model, get_backend("hip"), None, ps, 16, num_kv_blocks=300, enable_prefix_caching=False, **kw)
+    on, core = run_engine(model, get_backend("hip"), None, ps, 16, num_kv_blocks=300, **kw)
+    tight, core_t = run_engine(model, get_backend("hip"), None, ps, 16, num_kv_blocks=18, **kw)
+    assert_greedy_match(on, off)
+    assert_greedy_match(tight, off)
+    assert core.stats().prefix_cache_hits > 0 and core_t.stats().prefix_cache_hits > 0
