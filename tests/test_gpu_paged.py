@@ -336,3 +336,41 @@ def test_unsupported_shapes_raise(hip):
     wl = _kernel_case(dh=64)
     with pytest.raises(ValueError, match="head_dim"):
         hip_step(wl, DEV)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_maximum_sizes(hip, kv):
+    # a 65,536-token decode context (4,096 pages, 32+ splits merged), a 4,096-token prompt over 4,096
+    # cached tokens (64 query tiles, 128 key tiles each), and short rows beside them, on a shuffled pool
+    from minillm.workloads import Workload
+
+    g = torch.Generator().manual_seed(7)
+    h, hkv, dh, bs = 32, 8, 128, 16
+    steps = [(65535, 1), (4096, 4096), (0, 3), (17, 1), (100, 40)]
+    need = sum(-(-(c + n) // bs) for c, n in steps)
+    nb = need + 64
+    perm = torch.randperm(nb, generator=g).tolist()
+    seqs, o = [], 0
+    for c, n in steps:
+        k = -(-(c + n) // bs)
+        seqs.append((c, n, perm[o:o + k]))
+        o += k
+    n_tok = sum(n for _, n in steps)
+
+    def mk(*shape):
+        return torch.randn(*shape, generator=g).to(torch.bfloat16)
+
+    wl = Workload("max_sizes", seqs, nb, mk(n_tok, h, dh), mk(n_tok, hkv, dh), mk(n_tok, hkv, dh),
+                  mk(nb, bs, hkv, dh), mk(nb, bs, hkv, dh))
+    if kv == "bf16":
+        out, pk, pv, _ = hip_step(wl, DEV)
+        ref, rk, rv = oracle_step(wl, DEV)
+        assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    else:
+        from test_gpu_fp8 import fp8_step
+
+        out, pools, ref, exp = fp8_step(wl, 0.05, 0.05)
+        assert torch.equal(pools[0].view(torch.uint8), exp[0].view(torch.uint8))
+        assert torch.equal(pools[1].view(torch.uint8), exp[1].view(torch.uint8))
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
