@@ -144,6 +144,33 @@ __device__ __forceinline__ uint32_t pick_halves(uint32_t a, int ia, uint32_t b, 
   return __builtin_amdgcn_perm(a, b, sel_lo | (sel_hi << 16));
 }
 
+// ---------------------------------------------------------------- global -> LDS DMA and its waits
+
+__device__ __forceinline__ unsigned lds_offset(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// One DMA instruction (global_load_lds_dword{x4}): lane l's 16 (4) bytes at base + voff land at LDS
+// byte lds + 16 l (4 l).  base and lds are wave-uniform.  Issued from asm, so the compiler neither
+// counts these loads nor waits for them: every wait on them is an explicit vmcnt (barrier_vm).
+__device__ __forceinline__ void dma16(const char* base, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4(const char* base, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+
+// Workgroup barrier that first waits for this wavefront's LDS reads and for all but its N most recent
+// DMA loads (vmcnt retires loads in issue order).  One asm statement: the compiler moves no LDS access
+// across it and does not add the vmcnt(0) drain that __syncthreads' fence would (outstanding DMA
+// loads count as LDS writes to that fence).
+template <int N>
+__device__ __forceinline__ void barrier_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------- MFMA wrappers (gfx950)
 
 template <typename T>

@@ -29,7 +29,10 @@ namespace mllm {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kWaves = 4;  // KV heads per workgroup
+#ifndef MLLM_DECODE_WAVES
+#define MLLM_DECODE_WAVES 4
+#endif
+constexpr int kWaves = MLLM_DECODE_WAVES;  // KV heads per workgroup
 #ifndef MLLM_DECODE_LAZY_RESCALE
 #define MLLM_DECODE_LAZY_RESCALE 1
 #endif
@@ -320,9 +323,15 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
 // Tuned on MI355X (decode_256 workload): one tile of lookahead with non-temporal K/V loads at 3
 // wavefronts per SIMD streams at 6.2 TB/s, the same as a two-tile lookahead at 2 per SIMD; forcing 4
 // per SIMD spills.
-constexpr int kPrefetch = 1;
+#ifndef MLLM_DECODE_PREFETCH
+#define MLLM_DECODE_PREFETCH 1
+#endif
+#ifndef MLLM_DECODE_OCC
+#define MLLM_DECODE_OCC 3
+#endif
+constexpr int kPrefetch = MLLM_DECODE_PREFETCH;
 constexpr bool kNonTemporal = true;
-constexpr int kOccupancy = 3;
+constexpr int kOccupancy = MLLM_DECODE_OCC;
 // fp8 tiles hold half the bytes in half the registers: three tiles of lookahead (154 VGPRs, no spill)
 // measured 213-215 us on decode_256 against 219-226 us with two.
 #ifndef MLLM_DECODE_FP8_PREFETCH

@@ -93,19 +93,6 @@ __device__ __forceinline__ const char* group_base(const char* pool, const Prefil
 __device__ __forceinline__ int k_chunk(int r, int lane) { return (lane & 15) ^ (r & 15); }
 __device__ __forceinline__ int v_chunk(int r, int lane) { return (lane & 15) ^ (4 * (r & 3)); }
 
-__device__ __forceinline__ unsigned lds_offset(const void* p) {
-  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-// One DMA instruction (global_load_lds_dword{x4}): lane l's 16 (4) bytes at base + voff land at LDS
-// byte lds + 16 l (4 l).  base and lds are wave-uniform.  Issued from asm, so the compiler neither
-// counts these loads nor waits for them: every wait on them is an explicit vmcnt in a barrier below.
-__device__ __forceinline__ void dma16(const char* base, unsigned voff, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
-}
-__device__ __forceinline__ void dma4(const char* base, unsigned voff, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
-}
 
 // This wavefront's share (rows 8 w .. 8 w + 7) of the K or V tile starting at key kv0 into `slot`.
 // off0 / off1: the lanes' offsets from the group base for full tiles; IS_V selects the swizzle.
@@ -153,16 +140,6 @@ __device__ __forceinline__ void stage_store(u32x4 x, int w, int lane, char* slot
   *reinterpret_cast<u32x4*>(row + 16 * ((c0 + 1) ^ sw)) = fp8x8_to<T>(x[2], x[3]);
 }
 
-// Workgroup barrier that first waits for this wavefront's LDS reads and for all but its N most recent
-// DMA loads (vmcnt retires loads in issue order).  One asm statement: the compiler moves no LDS access
-// across it and does not add the vmcnt(0) drain that __syncthreads' fence would (outstanding DMA
-// loads count as LDS writes to that fence).
-template <int N>
-__device__ __forceinline__ void barrier_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // N = number of DMA instructions issued since the loads that must have landed (0, 2 or 4)
 __device__ __forceinline__ void barrier_vm_n(int n) {
   if (n >= 4)
