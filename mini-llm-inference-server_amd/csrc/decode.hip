@@ -37,6 +37,10 @@ constexpr int kWaves = MLLM_DECODE_WAVES;  // KV heads per workgroup
 #define MLLM_DECODE_LAZY_RESCALE 1
 #endif
 constexpr bool kLazyRescale = MLLM_DECODE_LAZY_RESCALE;
+#ifndef MLLM_DECODE_K_NT
+#define MLLM_DECODE_K_NT 1
+#endif
+constexpr bool kKNonTemporal = MLLM_DECODE_K_NT;  // K loads of 16-bit pools with the non-temporal hint
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -112,7 +116,7 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const char* kbase
     for (int i = 0; i < 4; ++i) r.v[i] = ldkv8<NT>(vp + (int64_t)i * tok_stride + 8 * c);
   } else {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) r.k[kk] = ldkv<NT>(kp + 2 * qk_dim0<false>(kk, g));
+    for (int kk = 0; kk < 4; ++kk) r.k[kk] = ldkv<NT && kKNonTemporal>(kp + 2 * qk_dim0<false>(kk, g));
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.v[i] = ldkv<NT>(vp + (int64_t)i * tok_stride + 16 * c);
   }
