@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MLLM_ABI_VERSION 1
+#define MLLM_ABI_VERSION 2
 
 #define MLLM_OK 0
 #define MLLM_ERR_INVALID (-1)
@@ -122,19 +122,23 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
 
 /*
  * Per-step work plan (the analogue of FlashInfer's plan(), which the reference runs once per step:
- * src/minillm/attention/flashinfer_backend.py:44-64).  Built on the GPU from qo_indptr / kv_indptr.
- *   decode rows (num_new == 1): split into chunks of pages_per_split pages; one int4 work item
- *     {seq, split, num_splits, first_item} each, in sequence order -> decode_work[num_decode_work];
- *     sequences with more than one split also get an int4 {seq, first_item, num_splits, 0}
- *     -> merge_work[num_merge_work].
- *   multi-token rows: one int2 item {seq, first_new_token} per tile of q_tile_tokens new tokens,
- *     last tile of each row first -> prefill_work[num_prefill_work].
+ * src/minillm/attention/flashinfer_backend.py:44-64).  Built on the GPU from qo_indptr / kv_indptr /
+ * seq_lens (tokens per row, cached + new).
+ *   decode rows (num_new == 1): split into ceil(P / pages_per_split) balanced chunks of pages; one int4
+ *     work item {seq, split, num_splits, first_item} each -> decode_work[num_decode_work], largest chunk
+ *     first; first_item numbers the row's chunks in sequence order (the partial slots of the merge).
+ *     Sequences with more than one split also get an int4 {seq, first_item, num_splits, 0}, in sequence
+ *     order -> merge_work[num_merge_work].
+ *   multi-token rows: one int2 item {seq, first_new_token} per tile of q_tile_tokens new tokens
+ *     -> prefill_work[num_prefill_work], across all rows in decreasing number of 64-key tiles that the
+ *     tile's causal context spans (the prefill kernel's work per item), so short items end the launch.
  * The caller computes the three counts from the same host facts (sequence lengths and new-token
  * counts); the kernel writes at most that many items.  pages_per_split <= 128.
  */
-int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, int32_t pages_per_split,
-              int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work,
-              int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work, void* stream);
+int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
+              int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
+              int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work,
+              void* stream);
 
 /*
  * mllm_plan with the split size read from device memory at run time (*pages_per_split, clamped to
@@ -143,10 +147,10 @@ int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_se
  * re-plans every replayed step.  The capacities must cover min_pages_per_split splits, so no item is ever
  * dropped; items past a step's own stay as the caller pre-filled them (-1).
  */
-int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, int32_t num_seqs, const int32_t* pages_per_split,
-                  int32_t min_pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
-                  int32_t* merge_work, int32_t num_merge_work, int32_t* prefill_work, int32_t num_prefill_work,
-                  void* stream);
+int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
+                  const int32_t* pages_per_split, int32_t min_pages_per_split, int32_t q_tile_tokens,
+                  int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work, int32_t num_merge_work,
+                  int32_t* prefill_work, int32_t num_prefill_work, void* stream);
 
 /* Bytes of fp32 split-KV partials the decode needs for num_decode_work items (0 if none split). */
 int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim);

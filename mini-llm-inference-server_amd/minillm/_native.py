@@ -16,7 +16,7 @@ LIB_PATH = Path(os.environ.get("MLLM_HIP_LIB", Path(__file__).resolve().parent /
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -36,8 +36,8 @@ SIGNATURES = {
                                       _p]),
     "mllm_rope_kv_append": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32, _i32,
                                            _i32, _i32, _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p]),
-    "mllm_plan": (ctypes.c_int, [_p, _p, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
-    "mllm_plan_dev": (ctypes.c_int, [_p, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
+    "mllm_plan": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
+    "mllm_plan_dev": (ctypes.c_int, [_p, _p, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
     "mllm_decode_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32]),
     "mllm_paged_decode": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                          _i32, _p, _i32, _i32, _f32, _i32, _p, _i64, _i64, _p, _i64, _p]),

@@ -262,12 +262,13 @@ class HipBackend(AttentionBackend):
         buf = torch.full((4 * n_dec + 4 * n_merge + 2 * n_pf,), -1, dtype=torch.int32, device=dev)
         dec, mrg, pf = buf[:4 * n_dec], buf[4 * n_dec:4 * (n_dec + n_merge)], buf[4 * (n_dec + n_merge):]
         if split_dev is not None:
-            self._lib.call("mllm_plan_dev", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs,
-                           split_dev.data_ptr(), c, q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf,
-                           stream)
+            self._lib.call("mllm_plan_dev", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(),
+                           meta.seq_lens_i32.data_ptr(), meta.num_seqs, split_dev.data_ptr(), c, q_tile, _ptr(dec),
+                           n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf, stream)
         else:
-            self._lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.num_seqs, c,
-                           q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge, _ptr(pf), n_pf, stream)
+            self._lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(),
+                           meta.seq_lens_i32.data_ptr(), meta.num_seqs, c, q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge,
+                           _ptr(pf), n_pf, stream)
         ws = self._lib.workspace_bytes(n_dec, h, dh) if n_merge else 0
         self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws)
         self._planned = meta

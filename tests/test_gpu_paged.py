@@ -288,9 +288,10 @@ def test_plan_is_reused_per_metadata(hip):
 
 
 def test_plan_contents(hip):
-    # the GPU plan against the split rule it implements, on rows of many lengths: a decode row of P
-    # pages gets ns = ceil(P / C) balanced splits with canonical partial slots; the launch order is
-    # largest split first
+    # the GPU plan against the rules it implements, on rows of many lengths: a decode row of P pages gets
+    # ns = ceil(P / C) balanced splits with canonical partial slots, launched largest split first; a
+    # prefill row gets one item per q_tile new tokens, launched in decreasing number of 64-key tiles its
+    # causal context spans
     from minillm.attention.hip_backend import HipBackend
     from minillm.attention.metadata import AttentionMetadata, SeqStep
 
@@ -329,7 +330,16 @@ def test_plan_contents(hip):
     sizes = [size(it) for it in dec]
     assert sizes == sorted(sizes, reverse=True) and max(sizes) <= c
     assert p.merge_work.view(-1, 4).cpu().tolist() == exp_merge
-    assert p.prefill_work.view(-1, 2).cpu().tolist() == exp_pf
+    pf = p.prefill_work.view(-1, 2).cpu().tolist()
+    assert sorted(pf) == sorted(exp_pf)
+
+    def tiles(item):
+        s, t0 = item
+        cached, n = steps[s]
+        return -(-(cached + min(t0 + p.q_tile, n)) // 64)
+
+    spans = [tiles(it) for it in pf]
+    assert spans == sorted(spans, reverse=True) and len(set(spans)) > 20
 
 
 def test_unsupported_shapes_raise(hip):

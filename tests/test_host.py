@@ -61,7 +61,7 @@ def test_argument_errors_map_to_value_error(libpath):
 
     lib = _native.lib()
     with pytest.raises(ValueError, match="pages_per_split"):
-        lib.call("mllm_plan", 0, 0, 1, 0, 32, 0, 0, 0, 0, 0, 0, 0)
+        lib.call("mllm_plan", 0, 0, 0, 1, 0, 32, 0, 0, 0, 0, 0, 0, 0)
     with pytest.raises(ValueError, match="head_dim"):
         lib.call("mllm_paged_decode", 0, 0, 0, 0, 0, 0, 16, 32, 8, 64, 0, 0, 0, 0, 0, 1, 0, 0, 8, 1.0, 2, 0, 0, 0, 0,
                  0, 0)
