@@ -16,6 +16,7 @@ host's cores on a bounded sample of the same rows.
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
     python bench.py --workload copy_1gib                      # counter calibration: a 1 GiB device copy
+    python bench.py --workload gemm_8192                      # attainable bf16 MFMA rate of a library GEMM
     python bench.py --kv-dtype fp8                            # the same step on an fp8 (e4m3fn) pool
 
 With --kv-dtype fp8 the pool holds the workload's values cast to e4m3fn (scale 1: the N(0, 1) data is
@@ -245,6 +246,37 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
 
 
+def gemm_calibration():
+    """The attainable bf16 MFMA rate of a library GEMM on this GPU: torch.mm (hipBLASLt) on 8192^3 bf16
+    operands, random N(0, 1) and all-zero (the clock the MFMA stream sustains depends on the data it
+    switches), each the mean of 20 launches after 5 warm-up ones."""
+    import torch
+
+    n = 8192
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    out = {"gemm": f"torch.mm bf16 {n}x{n}x{n}", "peak_tflops": BF16_PEAK_TFLOPS}
+    for name in ("random", "zeros"):
+        if name == "random":
+            a = torch.randn(n, n, generator=g, device="cuda:0", dtype=torch.bfloat16)
+            b = torch.randn(n, n, generator=g, device="cuda:0", dtype=torch.bfloat16)
+        else:
+            a = torch.zeros(n, n, device="cuda:0", dtype=torch.bfloat16)
+            b = torch.zeros_like(a)
+        for _ in range(5):
+            torch.mm(a, b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch.mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        out[f"{name}_us"] = round(ms * 1e3, 1)
+        out[f"{name}_tflops"] = round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -263,6 +295,8 @@ def main():
         return bench_engine(args)
     if args.workload == "copy_1gib":
         return copy_calibration()
+    if args.workload == "gemm_8192":
+        return gemm_calibration()
     dev = torch.device("cuda:0")
     wl = workloads.WORKLOADS[args.workload]()
     q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
