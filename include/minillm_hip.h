@@ -129,9 +129,10 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  *     first; first_item numbers the row's chunks in sequence order (the partial slots of the merge).
  *     Sequences with more than one split also get an int4 {seq, first_item, num_splits, 0}, in sequence
  *     order -> merge_work[num_merge_work].
- *   multi-token rows: one int2 item {seq, first_new_token} per tile of q_tile_tokens new tokens
- *     -> prefill_work[num_prefill_work], across all rows in decreasing number of 64-key tiles that the
- *     tile's causal context spans (the prefill kernel's work per item), so short items end the launch.
+ *   multi-token rows: one item per tile of q_tile_tokens new tokens, 8 int32 each:
+ *     {seq, first_new_token, qo_indptr[seq], new tokens of seq, cached tokens of seq, kv_indptr[seq],
+ *      keys visible to the tile's last token, 64-key tiles they span} -> prefill_work[8 * num_prefill_work],
+ *     across all rows in decreasing number of those tiles (the prefill kernel's work per item).
  * The caller computes the three counts from the same host facts (sequence lengths and new-token
  * counts); the kernel writes at most that many items.  pages_per_split <= 128.
  */

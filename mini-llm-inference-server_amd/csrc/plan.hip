@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
                                                             const int32_t* __restrict__ split_dev, int32_t q_tile,
                                                             int4* __restrict__ decode_work, int32_t cap_decode,
                                                             int4* __restrict__ merge_work, int32_t cap_merge,
-                                                            int2* __restrict__ prefill_work, int32_t cap_prefill) {
+                                                            int4* __restrict__ prefill_work, int32_t cap_prefill) {
   __shared__ int sums[kPlanThreads / 64];
   __shared__ int hist[kMaxSplitPages + 1];  // decode items per size in pages
   __shared__ int offs[kMaxSplitPages + 1];  // next free position of each size class
@@ -128,11 +128,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
       if (pos < cap_decode) decode_work[pos] = make_int4(s, j, nd, od + j);
     }
     if (nm && om < cap_merge) merge_work[om] = make_int4(s, od, nd, 0);
-    if (pf) {
-      const int nn = qo_indptr[s + 1] - qo_indptr[s], cached = seq_lens[s] - nn;
+    if (pf) {  // {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: what the prefill kernel reads per item
+      const int qs = qo_indptr[s], nn = qo_indptr[s + 1] - qs, cached = seq_lens[s] - nn, kv0 = kv_indptr[s];
       for (int t0 = 0; t0 < nn; t0 += q_tile) {
         const int pos = atomicAdd(&phist[prefill_class(cached, t0, nn, q_tile)], 1);
-        if (pos < cap_prefill) prefill_work[pos] = make_int2(s, t0);
+        const int kv_end = cached + min(t0 + q_tile, nn);
+        if (pos < cap_prefill) {
+          prefill_work[2 * pos] = make_int4(s, t0, qs, nn);
+          prefill_work[2 * pos + 1] = make_int4(cached, kv0, kv_end, (kv_end + kPrefillKeyTile - 1) / kPrefillKeyTile);
+        }
       }
     }
     base_d += td;
@@ -166,7 +170,7 @@ int plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_
   plan_kernel<<<1, kPlanThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       qo_indptr, kv_indptr, seq_lens, num_seqs, pages_per_split, split_dev, q_tile_tokens,
       reinterpret_cast<int4*>(decode_work), num_decode_work, reinterpret_cast<int4*>(merge_work), num_merge_work,
-      reinterpret_cast<int2*>(prefill_work), num_prefill_work);
+      reinterpret_cast<int4*>(prefill_work), num_prefill_work);
   return check_launch(fn);
 }
 

@@ -63,7 +63,7 @@ struct PrefillArgs {
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
   const int32_t* seq_lens;
-  const int2* work;
+  const int4* work;  // the plan's prefill records, two int4 each (see the kernel)
   int QT;
   float scale_log2;  // softmax scale x k_scale x log2(e)
   float v_scale;     // output scale of an fp8 pool
@@ -313,19 +313,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const int grp = wave >> 2;  // 0: matrix phase first; 1: vector phase first
   const int wu = __builtin_amdgcn_readfirstlane(wave);  // the same index, as a uniform value (load addressing)
   const int kvh = blockIdx.x % a.Hkv;
-  const int2 w = a.work[blockIdx.x / a.Hkv];
-  const int seq = w.x, t0 = w.y;
+  // plan record {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: new tokens t0 .. t0 + QT - 1 of row
+  // seq (qs: its first row in q; nn new tokens after `cached` cached ones; page ids from
+  // kv_indices[kv_start]); its rows see keys 0 .. kv_end - 1, ntiles 64-key tiles.  One scalar load.
+  const int4 w0 = a.work[2 * (blockIdx.x / a.Hkv)], w1 = a.work[2 * (blockIdx.x / a.Hkv) + 1];
+  const int seq = w0.x, t0 = w0.y, qs = w0.z, nn = w0.w, cached = w1.x;
   if (seq < 0) return;  // unfilled plan slot (the host pre-fills the plan with -1)
-  const int qs = a.qo_indptr[seq];
-  const int nn = a.qo_indptr[seq + 1] - qs;
-  const int len = a.seq_lens[seq];
-  const int cached = len - nn;
-  const int32_t* pages = a.kv_indices + a.kv_indptr[seq];
+  const int len = cached + nn;
+  const int32_t* pages = a.kv_indices + w1.y;
   const int tpw = 32 / a.G;  // tokens per wavefront
-  const int qt_valid = min(a.QT, nn - t0);
-  const int kv_end = min(len, cached + t0 + qt_valid);  // keys any row of this workgroup may see
+  const int kv_end = w1.z;   // keys any row of this workgroup may see
   const int last = kv_end - 1;
-  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const int ntiles = w1.w;
 
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + wave * tpw + n / a.G;  // new-token index within the row
@@ -365,22 +364,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   int wbase = 0, wsel = 0;
   auto blk_of = [&](int t) { return __builtin_amdgcn_readfirstlane(idwin[64 * wsel + t - wbase]); };
   load_ids(0, 0);
-
-  u32x4 qf[8];  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7
-  {
-    const int head = kvh * a.G + (n % a.G);
-    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
-      qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
-    }
-  }
-  // Q and the first id window have landed before any tile load goes out (the empty asm needs the Q
-  // registers, so the compiler's own wait for them is here, not behind the tile loads)
-  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
-               : "memory");
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // the first three tiles take their block ids from scalar loads, so their loads need not wait for the
+  // id window
+  auto blk_direct = [&](int t) { return pages[min(t * kBN + g16, last) >> a.bs_shift]; };
 
   f32x16 oacc[4];
 #pragma unroll
@@ -389,10 +375,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // prologue: K(0), V(0), K(1), V(1), K(2); K(0), V(0) and K(1) have landed after the first barrier
+  // prologue: K(0), V(0), K(1), V(1), K(2), then Q; all of them have landed after the first barrier
   if constexpr (F8) {
     for (int t = 0; t < min(ntiles, 3); ++t) {
-      const int b = blk_of(t);
+      const int b = blk_direct(t);
       const u32x4 kx = stage_load(kc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
       if (t < 2) {
         const u32x4 vx = stage_load(vc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
@@ -403,19 +389,32 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     barrier_vm<0>();
   } else {
     {
-      const int b0 = blk_of(0);
+      const int b0 = blk_direct(0);
       dma_tile<false>(kc, a, b0, 0, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(0));
       dma_tile<true>(vc, a, b0, 0, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(0));
     }
     if (ntiles > 1) {
-      const int b1 = blk_of(1);
+      const int b1 = blk_direct(1);
       dma_tile<false>(kc, a, b1, kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(1));
       dma_tile<true>(vc, a, b1, kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(1));
     }
     if (ntiles > 2)
-      dma_tile<false>(kc, a, blk_of(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(2));
-    barrier_vm_n(2 * (ntiles > 1) + 2 * (ntiles > 2));
+      dma_tile<false>(kc, a, blk_direct(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(2));
   }
+  // Q after the tile loads (its latency overlaps theirs); the wait for Q covers everything before it
+  u32x4 qf[8];  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7
+  {
+    const int head = kvh * a.G + (n % a.G);
+    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
+      qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
+               : "memory");
+  barrier_vm<0>();  // K(0), V(0), K(1), V(1), K(2), the id window and Q have landed
 
   STile st;
   u32x4 pf[2][2];
@@ -552,7 +551,7 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.kv_indptr = kv_indptr;
   a.kv_indices = kv_indices;
   a.seq_lens = seq_lens;
-  a.work = reinterpret_cast<const int2*>(prefill_work);
+  a.work = reinterpret_cast<const int4*>(prefill_work);
   a.QT = q_tile_tokens;
   a.scale_log2 = softmax_scale * k_scale * kLog2e;
   a.v_scale = v_scale;

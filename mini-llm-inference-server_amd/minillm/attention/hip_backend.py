@@ -262,7 +262,7 @@ class HipBackend(AttentionBackend):
         n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
         n_merge = sum(1 for p, nn in zip(pages, news) if nn == 1 and p > c)
         n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
-        buf = torch.full((4 * n_dec + 4 * n_merge + 2 * n_pf,), -1, dtype=torch.int32, device=dev)
+        buf = torch.full((4 * n_dec + 4 * n_merge + 8 * n_pf,), -1, dtype=torch.int32, device=dev)
         dec, mrg, pf = buf[:4 * n_dec], buf[4 * n_dec:4 * (n_dec + n_merge)], buf[4 * (n_dec + n_merge):]
         if split_dev is not None:
             self._lib.call("mllm_plan_dev", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(),

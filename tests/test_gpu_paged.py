@@ -330,15 +330,19 @@ def test_plan_contents(hip):
     sizes = [size(it) for it in dec]
     assert sizes == sorted(sizes, reverse=True) and max(sizes) <= c
     assert p.merge_work.view(-1, 4).cpu().tolist() == exp_merge
-    pf = p.prefill_work.view(-1, 2).cpu().tolist()
-    assert sorted(pf) == sorted(exp_pf)
-
-    def tiles(item):
-        s, t0 = item
-        cached, n = steps[s]
-        return -(-(cached + min(t0 + p.q_tile, n)) // 64)
-
-    spans = [tiles(it) for it in pf]
+    recs = p.prefill_work.view(-1, 8).cpu().tolist()
+    assert sorted(r[:2] for r in recs) == sorted(exp_pf)
+    starts = [0]
+    for _, n in steps:
+        starts.append(starts[-1] + n)
+    kv_starts = [0]
+    for c, n in steps:
+        kv_starts.append(kv_starts[-1] + -(-(c + n) // 16))
+    for s, t0, qs, nn, cached, kv0, kv_end, ntiles in recs:
+        c, n = steps[s]
+        assert (qs, nn, cached, kv0) == (starts[s], n, c, kv_starts[s])
+        assert kv_end == c + min(t0 + p.q_tile, n) and ntiles == -(-kv_end // 64)
+    spans = [r[7] for r in recs]
     assert spans == sorted(spans, reverse=True) and len(set(spans)) > 20
 
 
