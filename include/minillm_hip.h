@@ -192,7 +192,8 @@ int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t
  * chunk, bottom-right aligned over the cached prefix, K/V read through kv_indices.  QK^T and PV on
  * bf16/fp16 MFMA (32x32x16) with fp32 online softmax; the H/Hkv query heads of one KV head share
  * each K/V tile.  Work items from mllm_plan (prefill_work, q_tile_tokens = 256 / (H / Hkv)).
- * Same shape limits as mllm_paged_decode, and H / Hkv must divide 32.
+ * Same shape limits as mllm_paged_decode, and H / Hkv must divide 32; q, out and their row strides
+ * 16-byte aligned.
  */
 int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                        const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,

@@ -478,11 +478,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     }
   }
 
-  if (!row_valid) return;
+  // Output through LDS (the rings are idle after the loop's last barrier): the wavefront writes its 32
+  // rows x 128 dims into its own 8 KB, row-major with 16-byte chunk c of row r at chunk c ^ (r % 16),
+  // then stores whole 16-byte chunks, four rows per instruction (one token's G heads are adjacent rows,
+  // contiguous in out for the usual head stride).  Scattered 8-byte partial-line stores kept the
+  // workgroup from retiring for several microseconds.
   const float inv = (F8 ? a.v_scale : 1.f) / l_run;
-  const int head = kvh * a.G + (n % a.G);
-  uint16_t* orow = a.out + (int64_t)(qs + tok) * a.o_st + (int64_t)head * a.o_sh;
-  // oacc[dt][r]: dim 32 dt + 8 (r / 4) + 4 h + r % 4
+  char* ost = lds + wave * (32 * kRowBytes);
+  // oacc[dt][r]: dim 32 dt + 8 (r / 4) + 4 h + r % 4 of row n, i.e. chunk 4 dt + r / 4, half h
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -490,8 +493,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       const int r = 4 * g4;
       const u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
                              pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
-      st8(orow + 32 * dt + 8 * g4 + 4 * h, pk);
+      *reinterpret_cast<u32x2*>(ost + n * kRowBytes + 16 * ((4 * dt + g4) ^ (n & 15)) + 8 * h) = pk;
     }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4), chunk = lane & 15;  // lane's row of the wavefront and its chunk
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + row * kRowBytes + 16 * (chunk ^ (row & 15)));
+    const int rtok = t0 + wave * tpw + row / a.G;
+    if (rtok < nn) {
+      uint16_t* o = a.out + (int64_t)(qs + rtok) * a.o_st + (int64_t)(kvh * a.G + row % a.G) * a.o_sh;
+      *reinterpret_cast<u32x4*>(o + 8 * chunk) = v;
+    }
+  }
 }
 
 }  // namespace
@@ -525,9 +538,9 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   if (num_prefill_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && prefill_work,
                MLLM_ERR_INVALID, fn + ": null pointer");
-  const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)out % 8 == 0) && ((uintptr_t)k_cache % 16 == 0) &&
+  const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)out % 16 == 0) && ((uintptr_t)k_cache % 16 == 0) &&
                        ((uintptr_t)v_cache % 16 == 0) && (q_stride_tok * 2) % 16 == 0 &&
-                       (q_stride_head * 2) % 16 == 0 && (out_stride_tok * 2) % 8 == 0 && (out_stride_head * 2) % 8 == 0;
+                       (q_stride_head * 2) % 16 == 0 && (out_stride_tok * 2) % 16 == 0 && (out_stride_head * 2) % 16 == 0;
   MLLM_REQUIRE(aligned, MLLM_ERR_UNSUPPORTED, fn + ": q, out and pools need aligned rows");
   MLLM_REQUIRE((int64_t)num_prefill_work * num_kv_heads < (1ll << 31), MLLM_ERR_UNSUPPORTED,
                fn + ": too many work items");
