@@ -58,13 +58,9 @@ struct PrefillArgs {
   int64_t num_blocks;
   unsigned page_bytes;  // bytes of one block of one pool: bs * Hkv * Dh * 2 (< 2^32)
   int row_bytes;        // bytes of one token row: Hkv * Dh * 2 (< 2^24)
-  int bs, bs_shift, H, Hkv, G;
-  const int32_t* qo_indptr;
-  const int32_t* kv_indptr;
+  int bs, bs_shift, Hkv, G;
   const int32_t* kv_indices;
-  const int32_t* seq_lens;
   const int4* work;  // the plan's prefill records, two int4 each (see the kernel)
-  int QT;
   float scale_log2;  // softmax scale x k_scale x log2(e)
   float v_scale;     // output scale of an fp8 pool
   uint16_t* out;
@@ -557,15 +553,10 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.page_bytes = (unsigned)((int64_t)block_size * a.row_bytes);
   a.bs = block_size;
   a.bs_shift = __builtin_ctz((unsigned)block_size);
-  a.H = num_heads;
   a.Hkv = num_kv_heads;
   a.G = G;
-  a.qo_indptr = qo_indptr;
-  a.kv_indptr = kv_indptr;
-  a.kv_indices = kv_indices;
-  a.seq_lens = seq_lens;
+  a.kv_indices = kv_indices;  // qo_indptr, kv_indptr and seq_lens are folded into the plan's records
   a.work = reinterpret_cast<const int4*>(prefill_work);
-  a.QT = q_tile_tokens;
   a.scale_log2 = softmax_scale * k_scale * kLog2e;
   a.v_scale = v_scale;
   a.out = static_cast<uint16_t*>(out);
