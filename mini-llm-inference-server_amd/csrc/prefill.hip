@@ -314,7 +314,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // kv_indices[kv_start]); its rows see keys 0 .. kv_end - 1, ntiles 64-key tiles.  One scalar load.
   const int4 w0 = a.work[2 * (blockIdx.x / a.Hkv)], w1 = a.work[2 * (blockIdx.x / a.Hkv) + 1];
   const int seq = w0.x, t0 = w0.y, qs = w0.z, nn = w0.w, cached = w1.x;
-  if (seq < 0) return;  // unfilled plan slot (the host pre-fills the plan with -1)
+  // unfilled plan slot (the host pre-fills the plan with -1), or a row whose seq_lens did not cover its
+  // new tokens (no visible key: nothing to load; uniform, before any barrier)
+  if (seq < 0 || w1.z <= 0) return;
   const int len = cached + nn;
   const int32_t* pages = a.kv_indices + w1.y;
   const int tpw = 32 / a.G;  // tokens per wavefront
