@@ -346,6 +346,30 @@ def test_plan_contents(hip):
     assert spans == sorted(spans, reverse=True) and len(set(spans)) > 20
 
 
+def test_prefill_item_without_visible_keys_writes_nothing(hip):
+    # a plan record whose row has no visible key (kv_end 0: seq_lens below the new-token count, which the
+    # metadata build never produces) makes the workgroup return before any load; out keeps its sentinel
+    from minillm import _native
+
+    lib = _native.lib()
+    h, hkv, dh, bs, nb = 32, 8, 128, 16, 8
+    q = torch.randn(64, h, dh, device=DEV).to(torch.bfloat16)
+    pool = torch.zeros(nb, bs, hkv, dh, dtype=torch.bfloat16, device=DEV)
+    out = torch.full((64, h, dh), 7.0, dtype=torch.bfloat16, device=DEV)
+    qo = torch.tensor([0, 64], dtype=torch.int32, device=DEV)
+    kvp = torch.tensor([4, 8], dtype=torch.int32, device=DEV)
+    kvi = torch.arange(8, dtype=torch.int32, device=DEV)
+    lens = torch.tensor([0], dtype=torch.int32, device=DEV)
+    # {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}
+    rec = torch.tensor([0, 0, 0, 64, -64, 4, 0, 0], dtype=torch.int32, device=DEV)
+    lib.call("mllm_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), pool.data_ptr(), nb, bs,
+             h, hkv, dh, qo.data_ptr(), kvp.data_ptr(), kvi.data_ptr(), lens.data_ptr(), rec.data_ptr(), 1,
+             256 // (h // hkv), dh ** -0.5, _native.dtype_code(torch.bfloat16), out.data_ptr(), out.stride(0),
+             out.stride(1), _native.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+
+
 def test_unsupported_shapes_raise(hip):
     wl = _kernel_case(dh=64)
     with pytest.raises(ValueError, match="head_dim"):
