@@ -132,6 +132,22 @@ def test_group_sizes_and_blocks(hip, h, hkv, bs):
     _check(*fp8_step(wl, 0.02, 0.02))
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_random_mixed_steps(hip, seed):
+    # seeded random steps with every row kind at the Llama GQA shape, fp8 pools with random scales
+    import random
+
+    rng = random.Random(2000 + seed)
+    bs = rng.choice([16, 32])
+    steps = []
+    for _ in range(rng.randrange(4, 12)):
+        new = rng.choice([1, 1, 2, rng.randrange(3, 200), rng.randrange(200, 400)])
+        steps.append((rng.randrange(0, 900), new))
+    nb = sum(-(-(c + n) // bs) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, bs=bs, steps=steps, num_blocks=nb, seed=seed)
+    _check(*fp8_step(wl, rng.uniform(0.02, 0.5), rng.uniform(0.02, 0.5)))
+
+
 def _owned_slots(wl, include_new=True):
     used = torch.zeros(wl.num_blocks * wl.block_size, dtype=torch.bool)
     for c, n, blocks in wl.seqs:

@@ -255,6 +255,25 @@ def test_larger_blocks(hip, bs):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_random_mixed_steps(hip, seed):
+    # seeded random steps with every row kind (fresh and cached, one and many new tokens, lengths not
+    # page-aligned) at the Llama GQA shape: the prefill items of many lengths exercise the plan's
+    # longest-first order and record fields; pools bit-exact, outputs within tolerance of the oracle
+    rng = random.Random(1000 + seed)
+    bs = rng.choice([16, 32])
+    steps = []
+    for _ in range(rng.randrange(4, 14)):
+        new = rng.choice([1, 1, 1, 2, rng.randrange(3, 200), rng.randrange(200, 420)])
+        steps.append((rng.randrange(0, 900), new))
+    nb = sum(-(-(c + n) // bs) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, bs=bs, steps=steps, seed=seed, num_blocks=nb)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def test_llama_call_site_views(hip):
     # the model passes q[0].transpose(0, 1) of a [1, H, N, Dh] tensor: token stride Dh, head stride N*Dh
     from minillm.attention import get_backend
