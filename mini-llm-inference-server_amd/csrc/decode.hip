@@ -310,15 +310,36 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
   if (seq < 0) return;
   const int head = blockIdx.y;
   const int d = threadIdx.x;
-  float mmax = -INFINITY;
-  for (int j = 0; j < n; ++j) mmax = fmaxf(mmax, part_ml[(int64_t)(first + j) * H + head].x);
-  float lsum = 0.f, acc = 0.f;
-  for (int j = 0; j < n; ++j) {
-    const int64_t row = (int64_t)(first + j) * H + head;
-    const float2 ml = part_ml[row];
-    const float wgt = fast_exp2(ml.x - mmax);
-    lsum += wgt * ml.y;
-    acc += wgt * part_o[row * kHeadDim + d];
+  // one online pass over the splits, four at a time so that their loads are in flight together (a row
+  // has a few splits: one round trip instead of two per split); slots past n re-read split 0 of the
+  // group and weigh it 2^-inf = 0
+  constexpr int kGroup = 4;
+  float m = -INFINITY, lsum = 0.f, acc = 0.f;
+  for (int j0 = 0; j0 < n; j0 += kGroup) {
+    float2 ml[kGroup];
+    float o[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int64_t row = (int64_t)(first + (j0 + u < n ? j0 + u : j0)) * H + head;
+      ml[u] = part_ml[row];
+      o[u] = part_o[row * kHeadDim + d];
+    }
+    float mc = m;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      if (j0 + u >= n) ml[u].x = -INFINITY;
+      mc = fmaxf(mc, ml[u].x);
+    }
+    const float sc = fast_exp2(m - mc);  // 0 for the first group (m = -inf, lsum = acc = 0)
+    lsum *= sc;
+    acc *= sc;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const float wgt = fast_exp2(ml[u].x - mc);
+      lsum += wgt * ml[u].y;
+      acc += wgt * o[u];
+    }
+    m = mc;
   }
   const int qtok = qo_indptr[seq];
   out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = cvt1<T>(acc / lsum);
