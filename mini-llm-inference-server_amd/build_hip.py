@@ -28,8 +28,9 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # MFMA accumulators in VGPRs (the unified register file) rather than AGPRs keeps the attention loops
 # free of accumulator copies between the two register halves
 FILE_FLAGS = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for name in ("decode.hip", "prefill.hip")}
+# inline-asm diagnostics (e.g. a clobber of a reserved register such as m0) fail the build
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall",
-                "-Wno-unused-function"]
+                "-Wno-unused-function", "-Werror=inline-asm"]
 
 
 def hipcc() -> str:

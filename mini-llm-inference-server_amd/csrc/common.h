@@ -152,12 +152,14 @@ __device__ __forceinline__ unsigned lds_offset(const void* p) {
 
 // One DMA instruction (global_load_lds_dword{x4}): lane l's 16 (4) bytes at base + voff land at LDS
 // byte lds + 16 l (4 l).  base and lds are wave-uniform.  Issued from asm, so the compiler neither
-// counts these loads nor waits for them: every wait on them is an explicit vmcnt (barrier_vm).
+// counts these loads nor waits for them: every wait on them is an explicit vmcnt (barrier_vm).  The
+// LDS address goes in as an "{m0}" operand: the compiler itself loads m0 right before the instruction
+// and knows the register is read there, so no value it keeps in m0 is lost.
 __device__ __forceinline__ void dma16(const char* base, unsigned voff, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds));
 }
 __device__ __forceinline__ void dma4(const char* base, unsigned voff, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds));
 }
 
 // Workgroup barrier that first waits for this wavefront's LDS reads and for all but its N most recent
