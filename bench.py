@@ -1,23 +1,32 @@
 #!/usr/bin/env python3
 """Benchmark of the paged-attention hot path on one MI355X.
 
-Default workload (decode_256): one layer of a ragged decode step of Llama-3.1-8B's attention shape
+Headline workload (decode_256): one layer of a ragged decode step of Llama-3.1-8B's attention shape
 (32 query / 8 KV heads, head_dim 128, 16-token blocks, bf16) over 256 rows whose cached contexts are
 uniform in [128, 4096], one new token each, pool = 2x the pages with a shuffled assignment.  A step
 is KV append + split-KV paged decode + split merge, with the step's metadata and work plan built
 beforehand (they are built once per engine step and shared by all 32 layers; their cost is reported
-separately).  `value` is decode tokens/s of the 32-layer model: 256 / (32 x layer time).
+separately, as a median after a warm-up).  `value` is decode tokens/s of the 32-layer model:
+256 / (32 x layer time).
 
-Prints one JSON line with the roofline of the dominant kernel (the decode kernel: algorithmic bytes
-per launch / its mean duration from HIP events around each launch in the timed region) and a CPU
-baseline: the oracle's restatement of the reference torch backend (gather + SDPA, bf16) timed on this
-host's cores on a bounded sample of the same rows.
+The line carries the roofline of the dominant kernel (the decode kernel: algorithmic bytes per launch
+over its mean duration from HIP events around each launch in the timed region) and a CPU baseline:
+the oracle's restatement of the reference torch backend (write_kv, gather padded to the longest row,
+SDPA; bf16) over all 256 rows on this host's cores (torch.set_num_threads(os.cpu_count())), median of
+3 runs after a warm-up.  Under "configs" it also carries, from the same run, the other layer
+workloads on the GPU with their own kernels' rates and the same CPU baseline:
+  decode_4    4 rows (contexts 37/128/211/500 + 1): step and decode-launch time (latency-bound);
+  mixed_128   8 prefill + 120 decode rows: prefill launch TFLOP/s and fraction of the bf16 peak over
+              its own launch, decode launch GB/s, and the step with both launches overlapped;
+  prefix_64   64 rows over a shared 2,048-token prefix: prefill launch TFLOP/s and fraction;
+  decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction.
 
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
     python bench.py --workload copy_1gib                      # counter calibration: a 1 GiB device copy
     python bench.py --workload gemm_8192                      # attainable bf16 MFMA rate of a library GEMM
     python bench.py --kv-dtype fp8                            # the same step on an fp8 (e4m3fn) pool
+    python bench.py --workload prefix_64 --no-configs --no-cpu-baseline   # one workload alone (profiling)
 
 With --kv-dtype fp8 the pool holds the workload's values cast to e4m3fn (scale 1: the N(0, 1) data is
 well inside e4m3's range) and the step runs the _fp8 entry points; the algorithmic bytes count one
@@ -52,7 +61,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-rows", type=int, default=16)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="measure only --workload (no decode_4 / mixed_128 / prefix_64 / fp8 sub-lines)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (default: os.cpu_count())")
     ap.add_argument("--compare-oracle", action="store_true",
                     help="engine_8b: also run the engine with the oracle hot path and compare greedy tokens")
     ap.add_argument("--requests", type=int, default=128)
@@ -69,35 +80,58 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(wl, rows: int):
-    """The oracle (reference torch backend restated: write_kv, gather, SDPA; bf16) on this host's cores
-    over the first `rows` rows of the workload, same pool and tensors."""
+def cpu_model() -> str:
+    """The host CPU's model name, as lscpu prints it."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_step_seconds(wl, threads: int, reps: int = 3):
+    """The oracle (reference torch backend restated: write_kv, gather padded to the longest decode row,
+    SDPA; bf16) over every row of the workload on this host's CPU: median of `reps` runs after one
+    warm-up, in seconds per layer, and the run times."""
     import torch
 
     from harness import oracle_step
-    from minillm.workloads import Workload
 
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
-    sel = list(range(min(rows, len(wl.seqs))))
-    starts = [0]
-    for c, n, _ in wl.seqs:
-        starts.append(starts[-1] + n)
-    tok = [t for i in sel for t in range(starts[i], starts[i + 1])]
-    sub = Workload(wl.name + "_sample", [wl.seqs[i] for i in sel], wl.num_blocks, wl.q[tok], wl.k[tok], wl.v[tok],
-                   wl.pool_k, wl.pool_v)
-    oracle_step(sub, "cpu", dtype=torch.bfloat16)  # warm-up
-    times, t_end = [], time.perf_counter() + 20.0
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+    torch.set_num_threads(threads)
+    oracle_step(wl, "cpu", dtype=torch.bfloat16)  # warm-up
+    times = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        oracle_step(sub, "cpu", dtype=torch.bfloat16)
+        oracle_step(wl, "cpu", dtype=torch.bfloat16)
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    n_tok = len(tok)
-    return {"value": n_tok / (LAYERS * t), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {len(sel)} of {len(wl.seqs)} rows, one layer x {len(times)} reps (median "
-                      f"{t * 1e3:.1f} ms), scaled to {LAYERS} layers; effective "
-                      f"{sub.algorithmic_bytes() / t / 1e9:.2f} GB/s on the same algorithmic bytes"}
+    return statistics.median(times), times
+
+
+def cpu_threads(args) -> int:
+    return args.cpu_threads or os.cpu_count() or 1
+
+
+def cpu_baseline(wl, args):
+    """The CPU baseline of the headline line: every row of the workload, one layer, scaled to 32 layers."""
+    threads = cpu_threads(args)
+    t, times = cpu_step_seconds(wl, threads)
+    return {"value": wl.num_tokens / (LAYERS * t), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"all {len(wl.seqs)} rows of {wl.name}, one layer, median of {len(times)} runs after a "
+                      f"warm-up ({', '.join(f'{x * 1e3:.0f}' for x in times)} ms), scaled to {LAYERS} layers",
+            "layer_ms": round(t * 1e3, 2), "hbm_gbps_same_bytes": round(wl.algorithmic_bytes() / t / 1e9, 2),
+            "os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": cpu_model()}
 
 
 def rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v, reps=20):
@@ -277,66 +311,63 @@ def gemm_calibration():
     print(json.dumps(out), flush=True)
 
 
-def main():
-    args = parse()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build runs the paged hot path on a single MI355X "
-              "(sharding is described, not built); use --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
+def shared_step_costs(wl, backend, dev, reps: int = 10):
+    """Per-step costs shared by the 32 layers, host + GPU, median of `reps` after one warm-up each:
+    the metadata build with every table uploaded (AttentionMetadata.build) plus the GPU work plan, and
+    the same from the engine's resident tables in steady state (a step that allocated no new block:
+    only num_cached, num_new and row ids travel)."""
     import torch
 
-    from minillm import workloads
-    from minillm.attention.hip_backend import HipBackend
     from minillm.attention.metadata import AttentionMetadata, DeviceBlockTables, SeqStep
 
-    if args.workload == "engine_8b":
-        return bench_engine(args)
-    if args.workload == "copy_1gib":
-        return copy_calibration()
-    if args.workload == "gemm_8192":
-        return gemm_calibration()
-    dev = torch.device("cuda:0")
-    wl = workloads.WORKLOADS[args.workload]()
-    q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
-    pool_k, pool_v = wl.pool_k.to(dev), wl.pool_v.to(dev)
-    fp8 = args.kv_dtype == "fp8"
-    kv_elem = 1 if fp8 else 2
-    ks = vs = 1.0
-    if fp8:
-        pool_k, pool_v = pool_k.to(torch.float8_e4m3fn), pool_v.to(torch.float8_e4m3fn)
     seqs = [SeqStep(c, n, b) for c, n, b in wl.seqs]
-    backend = HipBackend()
-
-    # per-step costs shared by the 32 layers: metadata build (host + GPU) and the GPU work plan, with every
-    # table uploaded (AttentionMetadata.build) and from the engine's resident tables in steady state (a
-    # step that allocated no new block: only num_cached, num_new and row ids travel)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(5):
-        meta = AttentionMetadata.build(seqs, wl.block_size, dev)
-        backend._planned = None
-        backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
-    torch.cuda.synchronize()
-    meta_plan_ms = (time.perf_counter() - t0) / 5 * 1e3
     tables = DeviceBlockTables(len(seqs), max(len(s.block_ids) for s in seqs), dev)
     keys = list(range(len(seqs)))
-    tables.build(keys, seqs, wl.block_size)  # the first step uploads every table
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(5):
-        rmeta = tables.build(keys, seqs, wl.block_size)
-        backend._planned = None
-        backend.plan(rmeta, wl.h, wl.hkv, wl.dh, dev)
-    torch.cuda.synchronize()
-    resident_ms = (time.perf_counter() - t0) / 5 * 1e3
-    del rmeta
-    backend._planned = None
-    backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
 
-    out = torch.empty_like(q)
+    def full():
+        meta = AttentionMetadata.build(seqs, wl.block_size, dev)
+        backend.invalidate_plan()
+        backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+
+    def resident():
+        meta = tables.build(keys, seqs, wl.block_size)
+        backend.invalidate_plan()
+        backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+
+    out = {}
+    for name, fn in (("metadata_build_and_plan", full), ("resident_tables_build_and_plan", resident)):
+        fn()  # warm-up (the resident path's first call also uploads every table)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        out[name] = round(statistics.median(times) * 1e3, 3)
+    out["note"] = f"host + GPU, median of {reps} after a warm-up"
+    backend.invalidate_plan()
+    return out
+
+
+def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
+    """One layer's step on the GPU: KV append, decode + merge, prefill, launched one after another on
+    the current stream; `warmup` untimed steps, then `steps` timed ones between two synchronisations,
+    with HIP events on that stream around every decode and prefill launch.  Mixed workloads also time
+    the backend's own step (prefill launch on a second stream beside decode + merge)."""
+    import torch
+
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
+    pool_k, pool_v = wl.pool_k.to(dev), wl.pool_v.to(dev)
+    if fp8:
+        pool_k, pool_v = pool_k.to(torch.float8_e4m3fn), pool_v.to(torch.float8_e4m3fn)
+    ks = vs = 1.0
+    meta = AttentionMetadata.build([SeqStep(c, n, b) for c, n, b in wl.seqs], wl.block_size, dev)
+    backend.invalidate_plan()
     plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+    out = torch.empty_like(q)
 
     def step(ev=None):
         backend.append(k, v, pool_k, pool_v, meta, ks, vs)
@@ -354,28 +385,89 @@ def main():
             if ev is not None:
                 ev[3].record()
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-
-    # timed region: K steps between two synchronisations; per-launch events around the dominant kernels
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     start.record()
-    for i in range(args.steps):
+    for i in range(steps):
         step(evs[i])
     stop.record()
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - w0) * 1e3
-    step_ms = start.elapsed_time(stop) / args.steps
-    dec_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0
-    pf_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0
+    res = {"wall_ms": (time.perf_counter() - w0) * 1e3, "step_ms": start.elapsed_time(stop) / steps,
+           "dec_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0,
+           "pf_ms": statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0,
+           "plan": plan, "meta": meta, "tensors": (q, k, v, pool_k, pool_v)}
+    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step: prefill beside decode
+        def ostep():
+            backend.append(k, v, pool_k, pool_v, meta, ks, vs)
+            backend.attend(q, pool_k, pool_v, meta, out, ks, vs)
+
+        for _ in range(max(3, warmup)):
+            ostep()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            ostep()
+        b.record()
+        torch.cuda.synchronize()
+        res["overlap_step_ms"] = a.elapsed_time(b) / steps
+    return res
+
+
+def kernel_rates(wl, r, kv_elem: int) -> dict:
+    """Rates of the layer's launches over their own mean durations, against MI355X's published peaks."""
+    out = {"step_us": round(r["step_ms"] * 1e3, 2), "tokens": wl.num_tokens, "rows": len(wl.seqs)}
+    if r["dec_ms"]:
+        gbps = wl.decode_kernel_bytes(kv_elem) / (r["dec_ms"] * 1e-3) / 1e9
+        out.update(decode_us=round(r["dec_ms"] * 1e3, 2), decode_bytes=wl.decode_kernel_bytes(kv_elem),
+                   decode_gbps=round(gbps, 1), decode_frac_of_8tbps=round(gbps / HBM_PEAK_GBPS, 4))
+    if r["pf_ms"]:
+        tf = wl.prefill_flops() / (r["pf_ms"] * 1e-3) / 1e12
+        out.update(prefill_us=round(r["pf_ms"] * 1e3, 2), prefill_flops=wl.prefill_flops(),
+                   prefill_tflops=round(tf, 1), prefill_frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
+    if "overlap_step_ms" in r:
+        out["overlapped_step_us"] = round(r["overlap_step_ms"] * 1e3, 2)
+        out["overlapped_tokens_per_s_32_layers"] = round(wl.num_tokens / (LAYERS * r["overlap_step_ms"] * 1e-3), 1)
+    return out
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build runs the paged hot path on a single MI355X "
+              "(sharding is described, not built); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from minillm import workloads
+    from minillm.attention.hip_backend import HipBackend
+
+    if args.workload == "engine_8b":
+        return bench_engine(args)
+    if args.workload == "copy_1gib":
+        return copy_calibration()
+    if args.workload == "gemm_8192":
+        return gemm_calibration()
+    dev = torch.device("cuda:0")
+    wl = workloads.WORKLOADS[args.workload]()
+    fp8 = args.kv_dtype == "fp8"
+    kv_elem = 1 if fp8 else 2
+    backend = HipBackend()
+
+    shared = shared_step_costs(wl, backend, dev)
+    r = measure_layer(wl, backend, dev, args.steps, args.warmup, fp8)
+    plan, meta = r["plan"], r["meta"]
+    step_ms, dec_ms, pf_ms = r["step_ms"], r["dec_ms"], r["pf_ms"]
 
     n_rows = len(wl.seqs)
     step_bytes = wl.algorithmic_bytes(kv_elem)
-    per_layer_tok_s = wl.num_tokens / (step_ms * 1e-3)
     value = wl.num_tokens / (LAYERS * step_ms * 1e-3)
     if plan.num_decode:
         dec_bytes = wl.decode_kernel_bytes(kv_elem)
@@ -415,36 +507,37 @@ def main():
                    "pages_per_split": plan.pages_per_split, "decode_items": plan.num_decode,
                    "prefill_items": plan.num_prefill},
         "roofline": roofline,
-        "per_layer": {"tokens_per_s": round(per_layer_tok_s, 1), "algorithmic_bytes": step_bytes,
+        "per_layer": {"tokens_per_s": round(wl.num_tokens / (step_ms * 1e-3), 1), "algorithmic_bytes": step_bytes,
                       "hbm_gbps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
                       "hbm_frac": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                      "decode_us": round(dec_ms * 1e3, 2), "prefill_us": round(pf_ms * 1e3, 2),
-                      "prefill_tflops": round(wl.prefill_flops() / (pf_ms * 1e-3) / 1e12, 1) if pf_ms else None},
-        "per_step_shared_ms": {"metadata_build_and_plan": round(meta_plan_ms, 3),
-                               "resident_tables_build_and_plan": round(resident_ms, 3)},
-        "wall_ms_timed_region": round(wall_ms, 2),
+                      **kernel_rates(wl, r, kv_elem)},
+        "per_step_shared_ms": shared,
+        "wall_ms_timed_region": round(r["wall_ms"], 2),
     }
-    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step: prefill beside decode
-        def ostep():
-            backend.append(k, v, pool_k, pool_v, meta, ks, vs)
-            backend.attend(q, pool_k, pool_v, meta, out, ks, vs)
-
-        for _ in range(3):
-            ostep()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(args.steps):
-            ostep()
-        b.record()
-        torch.cuda.synchronize()
-        o_ms = a.elapsed_time(b) / args.steps
-        line["mixed_overlap"] = {"step_us": round(o_ms * 1e3, 2), "sequential_step_us": round(step_ms * 1e3, 2),
-                                 "tokens_per_s": round(wl.num_tokens / (LAYERS * o_ms * 1e-3), 1),
-                                 "note": "append, then the prefill launch on a second stream beside decode + merge"}
+    q, k, v, pool_k, pool_v = r["tensors"]
     line["rotary_append"] = rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v)
-    if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool
-        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_rows)
+    del r, q, k, v, pool_k, pool_v, meta, plan
+    if not args.no_configs:
+        # the other layer workloads, on the GPU in this run; each beside the same CPU baseline
+        configs = {}
+        subs = [(name, False) for name in ("decode_4", "mixed_128", "prefix_64") if name != wl.name]
+        if not fp8 and wl.name == "decode_256":
+            subs.append(("decode_256", True))
+        for name, sub_fp8 in subs:
+            swl = wl if name == wl.name else workloads.WORKLOADS[name]()
+            sr = measure_layer(swl, backend, dev, args.steps, args.warmup, sub_fp8)
+            entry = {"gpu": kernel_rates(swl, sr, 1 if sub_fp8 else 2)}
+            del sr
+            if not sub_fp8 and not args.no_cpu_baseline:
+                t, times = cpu_step_seconds(swl, cpu_threads(args))
+                entry["cpu"] = {"layer_ms": round(t * 1e3, 2), "runs_ms": [round(x * 1e3, 1) for x in times],
+                                "threads": cpu_threads(args), "kind": "port (oracle, bf16, all rows)",
+                                "tokens_per_s_32_layers": round(swl.num_tokens / (LAYERS * t), 2)}
+            configs[f"{name}_fp8" if sub_fp8 else name] = entry
+            torch.cuda.empty_cache()
+        line["configs"] = configs
+    if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool, every row
+        line["cpu_baseline"] = cpu_baseline(wl, args)
     print(json.dumps(line), flush=True)
 
 
