@@ -4,7 +4,9 @@
  * Every entry point takes raw device pointers, explicit sizes and element strides, and a HIP stream
  * (passed as void*), launches asynchronously on that stream and never synchronises the host.  The
  * library never allocates device memory: the caller (PyTorch, in the host package) owns every buffer,
- * including the decode workspace whose size mllm_decode_workspace_bytes() reports.
+ * including the decode workspace whose size mllm_decode_workspace_bytes() reports.  The one device
+ * memory of its own is the fixed scratch array of mllm_paged_decode_noalloc (64 MiB per GPU, part of
+ * the loaded code object).
  *
  * Status: 0 on success, negative on failure; mllm_last_error() then returns a per-thread message.
  *   MLLM_ERR_INVALID     malformed arguments            (the Python wrapper raises ValueError)
@@ -185,6 +187,26 @@ int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
 int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work, int32_t num_heads,
                       int32_t head_dim, const int32_t* qo_indptr, int32_t dtype, void* out, int64_t out_stride_tok,
                       int64_t out_stride_head, const void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * mllm_paged_decode followed by mllm_merge_splits, allocating nothing: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory (code under HIP-graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split-KV partials go to a fixed 64 MiB (67,108,864-byte)
+ * device array of this library instead of a caller workspace: each GPU the library runs on holds its
+ * own copy until the process ends, looked up on the first call on that device (the current device;
+ * the stream must belong to it).  A step whose partials need more
+ * (mllm_decode_workspace_bytes(num_decode_work, H, Dh) > 64 MiB when num_merge_work > 0; 4,032 items at
+ * H = 32, Dh = 128) is rejected with MLLM_ERR_INVALID.  Calls that overlap on one GPU (other streams or
+ * threads) share the array and race; calls in order on one stream do not.  Arguments and results are
+ * mllm_paged_decode's and mllm_merge_splits' (16-bit pools), bit for bit.
+ */
+int mllm_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                              const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr,
+                              const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                              const int32_t* decode_work, int32_t num_decode_work, const int32_t* merge_work,
+                              int32_t num_merge_work, int32_t pages_per_split, float softmax_scale, int32_t dtype,
+                              void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream);
 
 /*
  * Ragged prefill / mixed attention for rows with several new tokens (reference paged_torch_ref.py:61-73;

@@ -23,6 +23,9 @@
 // stream is the 16-bit one; k_scale is folded into the softmax scale and v_scale into the output.
 #include <math.h>
 
+#include <mutex>
+#include <string>
+
 #include "common.h"
 
 namespace mllm {
@@ -484,6 +487,28 @@ extern "C" int mllm_paged_decode_fp8(const void* q, int64_t q_stride_tok, int64_
                       out_stride_head, workspace, workspace_bytes, true, k_scale, v_scale, stream);
 }
 
+namespace {
+
+int launch_merge(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work, int32_t num_heads,
+                 const int32_t* qo_indptr, int32_t dtype, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                 const void* workspace, hipStream_t st) {
+  using namespace mllm;
+  const float* part_o = static_cast<const float*>(workspace);
+  const float2* part_ml = reinterpret_cast<const float2*>(static_cast<const char*>(workspace) +
+                                                          (int64_t)num_decode_work * num_heads * kHeadDim * 4);
+  dim3 grid(num_merge_work, num_heads);
+  const int4* merge = reinterpret_cast<const int4*>(merge_work);
+  if (dtype == MLLM_DTYPE_BF16)
+    merge_kernel<BF16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                  static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+  else
+    merge_kernel<F16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                 static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+  return check_launch("mllm_merge_splits");
+}
+
+}  // namespace
+
 extern "C" int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t num_decode_work,
                                  int32_t num_heads, int32_t head_dim, const int32_t* qo_indptr, int32_t dtype,
                                  void* out, int64_t out_stride_tok, int64_t out_stride_head, const void* workspace,
@@ -499,17 +524,88 @@ extern "C" int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_wo
   MLLM_REQUIRE(workspace_bytes >= mllm_decode_workspace_bytes(num_decode_work, num_heads, head_dim), MLLM_ERR_INVALID,
                "mllm_merge_splits: workspace too small");
   MLLM_REQUIRE(num_heads <= 65535, MLLM_ERR_UNSUPPORTED, "mllm_merge_splits: too many heads");
-  const float* part_o = static_cast<const float*>(workspace);
-  const float2* part_ml = reinterpret_cast<const float2*>(static_cast<const char*>(workspace) +
-                                                          (int64_t)num_decode_work * num_heads * head_dim * 4);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid(num_merge_work, num_heads);
-  const int4* merge = reinterpret_cast<const int4*>(merge_work);
-  if (dtype == MLLM_DTYPE_BF16)
-    merge_kernel<BF16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
-                                                  static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
-  else
-    merge_kernel<F16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
-                                                 static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
-  return check_launch("mllm_merge_splits");
+  return launch_merge(merge_work, num_merge_work, num_decode_work, num_heads, qo_indptr, dtype, out, out_stride_tok,
+                      out_stride_head, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------- decode + merge without allocation
+//
+// The split-KV partials live in `scratch`, a fixed device array of this library, instead of a workspace
+// the caller allocates.  Each GPU holds its own copy for the life of the process; its device address is
+// looked up once per device (hipGetSymbolAddress, with that device current) and kept in g_scratch_ptr.
+// Nothing in it needs to start at zero: every partial the merge reads is written by the decode launch
+// of the same call.  Calls that overlap on one GPU (two streams, two threads) share the array and race.
+
+namespace {
+
+constexpr int64_t kScratchBytes = 64ll << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on that device).
+int scratch_ptr(void** out) {
+  using namespace mllm;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MLLM_ERR_HIP, std::string("mllm_paged_decode_noalloc: hipGetDevice: ") +
+                                                     hipGetErrorString(e));
+  MLLM_REQUIRE(dev >= 0 && dev < kMaxDevices, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode_noalloc: device index too large");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MLLM_ERR_HIP, std::string("mllm_paged_decode_noalloc: hipGetSymbolAddress(scratch): ") +
+                                    hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MLLM_OK;
+}
+
+// Decode items whose partials fit in the scratch.
+int64_t noalloc_max_work(int32_t num_heads, int32_t head_dim) {
+  const int64_t per = mllm_decode_workspace_bytes(1, num_heads, head_dim);
+  return per > 0 ? kScratchBytes / per : 0;
+}
+
+}  // namespace
+
+extern "C" int mllm_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                         const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                         int32_t block_size, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                         const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                         const int32_t* kv_indices, const int32_t* seq_lens,
+                                         const int32_t* decode_work, int32_t num_decode_work,
+                                         const int32_t* merge_work, int32_t num_merge_work, int32_t pages_per_split,
+                                         float softmax_scale, int32_t dtype, void* out, int64_t out_stride_tok,
+                                         int64_t out_stride_head, void* stream) {
+  using namespace mllm;
+  MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID,
+               "mllm_paged_decode_noalloc: negative count");
+  const int64_t need = num_merge_work ? mllm_decode_workspace_bytes(num_decode_work, num_heads, head_dim) : 0;
+  MLLM_REQUIRE(need <= kScratchBytes, MLLM_ERR_INVALID,
+               "mllm_paged_decode_noalloc: the step's split partials need " + std::to_string(need) +
+                   " bytes, more than the " + std::to_string(kScratchBytes) + "-byte scratch (at most " +
+                   std::to_string(noalloc_max_work(num_heads, head_dim)) +
+                   " decode items when rows are split); use mllm_paged_decode with a workspace");
+  MLLM_REQUIRE(num_merge_work == 0 || merge_work, MLLM_ERR_INVALID, "mllm_paged_decode_noalloc: null merge_work");
+  if (num_decode_work == 0) return MLLM_OK;
+  void* ws = nullptr;
+  if (need) {
+    const int rc = scratch_ptr(&ws);
+    if (rc != MLLM_OK) return rc;
+  }
+  int rc = paged_decode(q, q_stride_tok, q_stride_head, k_cache, v_cache, num_blocks, block_size, num_heads,
+                        num_kv_heads, head_dim, qo_indptr, kv_indptr, kv_indices, seq_lens, decode_work,
+                        num_decode_work, merge_work, num_merge_work, pages_per_split, softmax_scale, dtype, out,
+                        out_stride_tok, out_stride_head, ws, need, false, 1.f, 1.f, stream);
+  if (rc != MLLM_OK || num_merge_work == 0) return rc;
+  MLLM_REQUIRE(num_heads <= 65535, MLLM_ERR_UNSUPPORTED, "mllm_paged_decode_noalloc: too many heads");
+  return launch_merge(merge_work, num_merge_work, num_decode_work, num_heads, qo_indptr, dtype, out, out_stride_tok,
+                      out_stride_head, ws, reinterpret_cast<hipStream_t>(stream));
 }

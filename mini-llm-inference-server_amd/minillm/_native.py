@@ -42,6 +42,9 @@ SIGNATURES = {
     "mllm_paged_decode": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                          _i32, _p, _i32, _i32, _f32, _i32, _p, _i64, _i64, _p, _i64, _p]),
     "mllm_merge_splits": (ctypes.c_int, [_p, _i32, _i32, _i32, _i32, _p, _i32, _p, _i64, _i64, _p, _i64, _p]),
+    # decode + merge with the partials in the library's own scratch array (no allocation)
+    "mllm_paged_decode_noalloc": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
+                                                 _p, _i32, _p, _i32, _i32, _f32, _i32, _p, _i64, _i64, _p]),
     "mllm_paged_prefill": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                           _i32, _i32, _f32, _i32, _p, _i64, _i64, _p]),
     "mllm_dense_attention": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
