@@ -1,11 +1,16 @@
-"""Prefix-cache index: full pool blocks named by a chained SHA-256 of their tokens
-(reference src/minillm/cache/prefix.py:21-76; byte layout fixed by docs/decisions/08-block-hash-spec.md).
+"""Prefix cache: full pool blocks named by a chained SHA-256 of their tokens, so requests with the same
+leading tokens share those blocks' K/V (the shared-prefix pages the prefill kernel reads from many block
+tables).
 
+The names are a published byte format (reference docs/decisions/08-block-hash-spec.md; reference
+src/minillm/cache/prefix.py:21-35), kept bit for bit:
   root  = SHA-256("minillm-kv-v1" || 0x00 || canonical JSON of the salt keys)
   block = SHA-256(parent || the block's tokens as little-endian uint32)
 
-Requests whose leading blocks hash alike share those blocks (the shared-prefix pages the prefill
-kernel reads from many block tables).  Ownership and eviction order belong to the block manager.
+The index is this build's own: a dict from name to block id, and the reverse as a list indexed by block
+id (block ids are dense, 0 .. pool size - 1).  The first block to carry a name keeps it; a second block
+computed with the same contents at the same time stays private to its request.  Holders and eviction
+order belong to the block manager, which drops a block's name when it reuses the block.
 """
 
 from __future__ import annotations
@@ -27,48 +32,53 @@ def block_hash(parent: bytes, tokens: list[int]) -> bytes:
 
 
 def extend_chain(chain: list[bytes], root: bytes, tokens: list[int], num_blocks: int, block_size: int) -> None:
-    """Append hashes to `chain` until it names the first `num_blocks` full blocks of `tokens`."""
-    while len(chain) < num_blocks:
-        i = len(chain)
-        parent = chain[-1] if chain else root
-        chain.append(block_hash(parent, tokens[i * block_size:(i + 1) * block_size]))
+    """Grows `chain` in place until it names the first `num_blocks` full blocks of `tokens`."""
+    parent = chain[-1] if chain else root
+    for i in range(len(chain), num_blocks):
+        parent = block_hash(parent, tokens[i * block_size:(i + 1) * block_size])
+        chain.append(parent)
 
 
 class PrefixCache:
     def __init__(self) -> None:
-        self._by_hash: dict[bytes, int] = {}
-        self._by_block: dict[int, bytes] = {}
-        self.queries = 0  # prompt tokens looked up
-        self.hits = 0  # of those, tokens served from cached blocks
+        self._block_by_name: dict[bytes, int] = {}
+        self._name_by_block: list[bytes | None] = []
+        # token accounting the engine reports (hit rate = hits / queries)
+        self.queries = 0  # prompt tokens looked up at admission
+        self.hits = 0  # of those, tokens whose K/V came from named blocks
 
     def __len__(self) -> int:
-        return len(self._by_hash)
+        return len(self._block_by_name)
 
-    def lookup(self, hashes: list[bytes]) -> list[int]:
-        """Blocks of the longest cached prefix of `hashes`."""
-        found = []
-        for h in hashes:
-            b = self._by_hash.get(h)
+    def lookup(self, chain: list[bytes]) -> list[int]:
+        """Blocks named by the longest leading run of `chain` that the index knows."""
+        blocks: list[int] = []
+        get = self._block_by_name.get
+        for name in chain:
+            b = get(name)
             if b is None:
-                break
-            found.append(b)
-        return found
+                return blocks
+            blocks.append(b)
+        return blocks
 
-    def insert(self, h: bytes, block: int) -> None:
-        """Name a block that just filled; the first block to hold a prefix stays its cached copy."""
-        if h in self._by_hash or block in self._by_block:
+    def insert(self, name: bytes, block: int) -> None:
+        """Names a block that just filled, unless the name or the block is taken already."""
+        if name in self._block_by_name or self.is_cached(block):
             return
-        self._by_hash[h] = block
-        self._by_block[block] = h
+        if block >= len(self._name_by_block):
+            self._name_by_block.extend([None] * (block + 1 - len(self._name_by_block)))
+        self._name_by_block[block] = name
+        self._block_by_name[name] = block
 
     def is_cached(self, block: int) -> bool:
-        return block in self._by_block
+        return block < len(self._name_by_block) and self._name_by_block[block] is not None
 
     def forget(self, block: int) -> None:
-        h = self._by_block.pop(block, None)
-        if h is not None:
-            del self._by_hash[h]
+        """Drops the block's name (it is about to hold other K/V)."""
+        if self.is_cached(block):
+            del self._block_by_name[self._name_by_block[block]]
+            self._name_by_block[block] = None
 
     def clear(self) -> None:
-        self._by_hash.clear()
-        self._by_block.clear()
+        self._block_by_name.clear()
+        self._name_by_block.clear()

@@ -62,16 +62,18 @@ class DecodeGraphs:
     def bucket(self, num_rows: int) -> int:
         return next(b for b in self.buckets if b >= num_rows)
 
-    def run(self, keys, seqs: list[SeqStep], token_ids: list[int]) -> list[int]:
+    def run(self, keys, seqs: list[SeqStep], token_ids: list[int]) -> tuple[torch.Tensor, torch.Tensor]:
         """One decode step: `seqs` are the rows (one new token each, its id in `token_ids`), `keys` their
-        requests' keys in the resident tables.  Returns each row's greedy next token."""
-        b = self.bucket(len(seqs))
+        requests' keys in the resident tables.  Returns the rows' logits [rows, vocab] and greedy next
+        tokens [rows], views of the graph's output buffers (valid until its next replay)."""
+        n = len(seqs)
+        b = self.bucket(n)
         c = self.captured(b)
         self._stage(c, keys, seqs, token_ids)
         c.graph.replay()
         self.replays += 1
         self.last_bucket = b
-        return c.tokens[:len(seqs)].tolist()
+        return c.logits[:n], c.tokens[:n]
 
     def captured(self, bucket: int) -> _Captured:
         if bucket not in self._captured:

@@ -1,18 +1,26 @@
-"""Iteration-level scheduler over the paged pool (reference src/minillm/engine/scheduler.py:77-187).
+"""Iteration-level scheduler over the paged pool: which requests run in a step, and with how many new
+tokens each.  Bookkeeping only (block ids, counters), no tensors.
 
-Each step is either a prefill step (admit waiting requests FCFS, without skipping, while the batch,
-the token budget and the pool allow, keeping one block in reserve for every request whose next token
-starts a new block) or a decode step for every running request (a request at a block boundary gets
-one more block; when none is free the newest request is preempted and requeued at the front, to be
-recomputed).  With a prefix cache, an admitted request reuses the cached blocks of its longest named
-prefix and only the rest is prefilled.  Bookkeeping only: block ids, no tensors.
+Rules (reference src/minillm/engine/scheduler.py:77-187 and docs/decisions/09-scheduler-policy.md state
+them; the code is this build's own):
+- a step is a prefill step while waiting requests can be admitted, else a decode step of every running
+  request;
+- admission is first come, first served, without skipping: it stops at the first waiting request that
+  does not fit.  A request fits when fewer than `max_num_seqs` run, its tokens to compute fit the step's
+  budget (the first request of a step always does), and the pool can give it every block its tokens
+  need plus one spare block for each running or admitted request whose next token opens a new block;
+- a prefix-cache hit shares the named blocks of the request's longest named prefix (its last token is
+  always computed, so the step has logits to sample);
+- a decode step first gives every running request at a block boundary one more block, oldest first;
+  when the pool is empty the newest running request is preempted (its blocks released, its progress
+  dropped) and put back at the front of the queue, to be recomputed when readmitted.
 
-With `chunked_prefill` a step mixes both kinds (the reference's planned M7:
-docs/decisions/09-scheduler-policy.md, "Mixed prefill + decode steps"): every decoding request gets
-its one token, then requests still inside their prompt get their next chunk (oldest first), then
-waiting requests are admitted FCFS into what is left of the token budget, each with a first chunk.
-A chunk that stops before a request's last uncached token samples nothing; the prompt continues on top
-of its own cached tokens next step (reference tests/test_paged.py:142-146).
+With `chunked_prefill` a step mixes both kinds (the reference's planned M7: docs/decisions/09-scheduler-
+policy.md, "Mixed prefill + decode steps"): every decoding request gets its one token, then requests
+still inside their prompt get their next chunk (oldest first), then waiting requests are admitted FCFS
+into what is left of the token budget, each with a first chunk.  A chunk that stops short of a request's
+last uncached token samples nothing; the prompt continues on top of its own cached tokens next step
+(reference tests/test_paged.py:142-146).
 """
 
 from __future__ import annotations
@@ -24,7 +32,7 @@ from ..cache.prefix import extend_chain
 from .block_manager import BlockManager
 
 
-@dataclass(eq=False)
+@dataclass(eq=False)  # requests are compared by identity
 class Request:
     req_id: str
     prompt: list[int]
@@ -32,20 +40,23 @@ class Request:
     stop_ids: frozenset
     timeline: dict
     output: list[int] = field(default_factory=list)
-    block_ids: list[int] = field(default_factory=list)
-    num_cached: int = 0  # tokens whose k/v are in the pool
+    block_ids: list[int] = field(default_factory=list)  # the block table, while it holds K/V
+    num_cached: int = 0  # leading tokens whose K/V are in the pool
     num_preemptions: int = 0
-    root: bytes = b""
-    block_hashes: list[bytes] = field(default_factory=list)
-    num_named: int = 0  # leading blocks already named in the prefix cache
-    num_cached_tokens: int | None = None  # prompt tokens served from the cache at first admission
+    root: bytes = b""  # salted root of its prefix-hash chain
+    block_hashes: list[bytes] = field(default_factory=list)  # names of its leading full blocks, as computed
+    num_named: int = 0  # leading blocks of its table already named in the prefix cache
+    num_cached_tokens: int | None = None  # prompt tokens served from the cache at its first admission
 
     @property
     def num_tokens(self) -> int:
         return len(self.prompt) + len(self.output)
 
     def uncached(self) -> list[int]:
-        return (self.prompt + self.output)[self.num_cached:]
+        """The tokens whose K/V are not in the pool yet (prompt and output alike)."""
+        n = len(self.prompt)
+        c = self.num_cached
+        return self.prompt[c:] + self.output if c <= n else self.output[c - n:]
 
 
 @dataclass
@@ -60,6 +71,22 @@ class SchedulerOutput:
         return [(r, self.chunks[r]) for r in self.decode + self.prefill]
 
 
+@dataclass
+class _Claim:
+    """What admitting one request takes: the named blocks it shares and what else the pool must give."""
+
+    req: Request
+    shared: list[int]  # blocks of its longest named prefix
+    compute: int  # tokens to run through the model
+    new_blocks: int  # blocks to allocate for the rest
+    revived: int  # shared blocks nobody holds (they leave the pool's free count)
+    spare: int  # 1 when its first sampled token opens a new block
+
+    @property
+    def pool_cost(self) -> int:
+        return self.new_blocks + self.revived + self.spare
+
+
 class Scheduler:
     def __init__(self, max_num_seqs: int, max_num_batched_tokens: int, blocks: BlockManager, prefix=None,
                  chunked_prefill: bool = False) -> None:
@@ -69,7 +96,7 @@ class Scheduler:
         self.prefix = prefix
         self.chunked_prefill = chunked_prefill
         self.waiting: deque[Request] = deque()
-        self.running: list[Request] = []  # admission order, newest last
+        self.running: list[Request] = []  # admission order: the newest is last
         self.num_preemptions = 0
 
     def add(self, req: Request) -> None:
@@ -77,151 +104,153 @@ class Scheduler:
 
     def schedule(self) -> SchedulerOutput:
         if self.chunked_prefill:
-            return self._schedule_mixed()
-        admitted = self._admit()
+            return self._mixed_step()
+        admitted = self._admit_prefills()
         if admitted:
-            return SchedulerOutput(prefill=admitted, decode=[], chunks={r: len(r.uncached()) for r in admitted})
-        preempted = self._grow_running()
-        return SchedulerOutput(prefill=[], decode=list(self.running), preempted=preempted,
-                               chunks={r: 1 for r in self.running})
+            return SchedulerOutput(admitted, [], chunks={r: r.num_tokens - r.num_cached for r in admitted})
+        preempted = self._make_room()
+        return SchedulerOutput([], list(self.running), preempted, {r: 1 for r in self.running})
 
-    def _at_boundary(self, req: Request) -> bool:
-        return req.num_cached >= len(req.block_ids) * self.blocks.block_size
+    # ------------------------------------------------------------------ admission
 
-    def _decoding(self, req: Request) -> bool:
-        """Past its prompt: one uncached token, the last sampled one."""
-        return req.num_tokens - req.num_cached == 1 and bool(req.output)
+    def _claim(self, req: Request) -> _Claim:
+        bs = self.blocks.block_size
+        shared = self._longest_named_prefix(req)
+        total = self.blocks.blocks_for(req.num_tokens)
+        return _Claim(req, shared, compute=req.num_tokens - len(shared) * bs, new_blocks=total - len(shared),
+                      revived=sum(1 for b in shared if self.blocks.is_cached_unheld(b)),
+                      spare=int(req.num_tokens == total * bs))
 
-    def _admit(self) -> list[Request]:
-        reserve = sum(1 for r in self.running if self._at_boundary(r))
+    def _grant(self, claim: _Claim) -> None:
+        """Moves the claimed request into the running set with its block table."""
+        req, bs = claim.req, self.blocks.block_size
+        self.blocks.acquire(claim.shared)  # first, so that the allocation below cannot evict them
+        req.block_ids = claim.shared + self.blocks.allocate(claim.new_blocks)
+        req.num_cached = len(claim.shared) * bs
+        req.num_named = len(claim.shared)
+        if req.num_cached_tokens is None:
+            req.num_cached_tokens = req.num_cached
+        if self.prefix is not None:
+            self.prefix.queries += req.num_tokens
+            self.prefix.hits += req.num_cached
+        self.running.append(req)
+
+    def _open_block_count(self) -> int:
+        """Running requests whose next token, as of the last step, opens a new block."""
+        bs = self.blocks.block_size
+        return sum(1 for r in self.running if r.num_cached >= len(r.block_ids) * bs)
+
+    def _admit_prefills(self) -> list[Request]:
+        reserve = self._open_block_count()
+        tokens = 0
         admitted: list[Request] = []
-        budget_used = 0
-        for req in list(self.waiting):
-            if len(self.running) == self.max_num_seqs:
-                break
-            taken = self._take(req, reserve, None if not admitted else self.max_num_batched_tokens - budget_used)
-            if taken is None:
-                break
-            to_compute, spare = taken
-            reserve += spare
-            budget_used += to_compute
-            admitted.append(req)
-        for req in admitted:
-            self.waiting.remove(req)
+        while self.waiting and len(self.running) < self.max_num_seqs:
+            claim = self._claim(self.waiting[0])
+            over_budget = admitted and tokens + claim.compute > self.max_num_batched_tokens
+            if over_budget or claim.pool_cost + reserve > self.blocks.num_free:
+                break  # FCFS: nothing behind the head of the queue goes first
+            self._grant(claim)
+            admitted.append(self.waiting.popleft())
+            reserve += claim.spare
+            tokens += claim.compute
         return admitted
 
-    def _take(self, req: Request, reserve: int, budget: int | None) -> tuple[int, int] | None:
-        """Admits `req` into the running set when its tokens fit `budget` (None: no limit) and the pool
-        has blocks for all its tokens plus `reserve`; returns (tokens to compute, spare blocks it reserves)."""
-        bs = self.blocks.block_size
-        n = req.num_tokens
-        hits = self._lookup(req)
-        to_compute = n - len(hits) * bs
-        if budget is not None and to_compute > budget:
-            return None
-        total = self.blocks.blocks_for(n)
-        need = total - len(hits)
-        revive = sum(1 for b in hits if self.blocks.is_cached_unheld(b))
-        spare = 1 if n == total * bs else 0  # its first decode token will start a new block
-        if need + revive + spare + reserve > self.blocks.num_free:
-            return None
-        self.blocks.acquire(hits)
-        req.block_ids = hits + self.blocks.allocate(need)
-        req.num_cached = len(hits) * bs
-        req.num_named = len(hits)
-        if self.prefix is not None:
-            self.prefix.queries += n
-            self.prefix.hits += len(hits) * bs
-        if req.num_cached_tokens is None:
-            req.num_cached_tokens = len(hits) * bs
-        self.running.append(req)
-        return to_compute, spare
-
-    def _schedule_mixed(self) -> SchedulerOutput:
-        preempted = self._grow_running()
+    def _mixed_step(self) -> SchedulerOutput:
+        preempted = self._make_room()
         budget = self.max_num_batched_tokens
-        decode = [r for r in self.running if self._decoding(r)][:budget]
+        decode = [r for r in self.running if r.output and r.num_tokens - r.num_cached == 1][:budget]
         chunks = {r: 1 for r in decode}
         budget -= len(decode)
         prefill = []
         for r in self.running:  # prompts already under way, oldest first
             if r in chunks or budget == 0:
                 continue
-            n = min(budget, len(r.uncached()))
+            n = min(budget, r.num_tokens - r.num_cached)
             chunks[r], budget = n, budget - n
             prefill.append(r)
-        # FCFS admission into the rest of the budget; one block of reserve for every running request
-        # whose next sampled token starts a new block
+        # FCFS admission into the rest of the budget, with one spare block for every running request
+        # whose next sampled token opens a new block
         bs = self.blocks.block_size
         reserve = sum(1 for r in self.running if len(r.block_ids) * bs <= r.num_tokens)
         while self.waiting and budget > 0 and len(self.running) < self.max_num_seqs:
-            req = self.waiting[0]
-            taken = self._take(req, reserve, None)
-            if taken is None:
+            claim = self._claim(self.waiting[0])
+            if claim.pool_cost + reserve > self.blocks.num_free:
                 break
-            self.waiting.popleft()
-            n = min(budget, len(req.uncached()))
+            self._grant(claim)
+            req = self.waiting.popleft()
+            n = min(budget, claim.compute)
             chunks[req], budget = n, budget - n
-            reserve += taken[1]
+            reserve += claim.spare
             prefill.append(req)
-        return SchedulerOutput(prefill=prefill, decode=decode, preempted=preempted, chunks=chunks)
+        return SchedulerOutput(prefill, decode, preempted, chunks)
 
-    def _lookup(self, req: Request) -> list[int]:
-        """Cached blocks of the request's first (num_tokens - 1) tokens: the last token is always
-        computed, so the step has logits to sample."""
+    # ------------------------------------------------------------------ prefix cache
+
+    def _longest_named_prefix(self, req: Request) -> list[int]:
+        """Named blocks covering the request's first num_tokens - 1 tokens, as far as the cache knows them."""
         if self.prefix is None:
             return []
         bs = self.blocks.block_size
         k = (req.num_tokens - 1) // bs
-        if k == 0:
+        if k <= 0:
             return []
         extend_chain(req.block_hashes, req.root, req.prompt + req.output, k, bs)
         return self.prefix.lookup(req.block_hashes[:k])
 
     def name_full_blocks(self, reqs: list[Request]) -> None:
+        """After a step: names every block of `reqs` that its K/V filled since it was last named."""
         if self.prefix is None:
             return
         bs = self.blocks.block_size
         for req in reqs:
             full = req.num_cached // bs
-            if full <= req.num_named:
-                continue
-            extend_chain(req.block_hashes, req.root, req.prompt + req.output, full, bs)
-            for j in range(req.num_named, full):
-                self.prefix.insert(req.block_hashes[j], req.block_ids[j])
-            req.num_named = full
+            if full > req.num_named:
+                extend_chain(req.block_hashes, req.root, req.prompt + req.output, full, bs)
+                for j in range(req.num_named, full):
+                    self.prefix.insert(req.block_hashes[j], req.block_ids[j])
+                req.num_named = full
 
-    def _grow_running(self) -> list[Request]:
+    # ------------------------------------------------------------------ growth and preemption
+
+    def _make_room(self) -> list[Request]:
+        """One more block for every running request at a block boundary, oldest first, preempting from the
+        newest end while the pool is empty; returns the preempted requests, newest first."""
+        bs = self.blocks.block_size
         preempted: list[Request] = []
-        for req in list(self.running):  # oldest first
-            if req not in self.running or not self._at_boundary(req):
-                continue
-            while self.blocks.num_free == 0:
-                victim = self.running[-1]
-                self._preempt(victim)
-                preempted.append(victim)
-                if victim is req:
+        i = 0
+        while i < len(self.running):
+            req = self.running[i]
+            if req.num_cached >= len(req.block_ids) * bs:
+                while self.blocks.num_free == 0 and i < len(self.running):
+                    preempted.append(self._requeue_newest())
+                if i >= len(self.running):  # `req` itself went back to the queue, and all newer ones
                     break
-            if req in self.running:
-                req.block_ids += self.blocks.allocate(1)
+                req.block_ids.extend(self.blocks.allocate(1))
+            i += 1
         return preempted
 
-    def _preempt(self, req: Request) -> None:
-        self.running.remove(req)
-        self.blocks.free(req.block_ids)
-        req.num_cached = req.num_named = 0
-        req.num_preemptions += 1
+    def _requeue_newest(self) -> Request:
+        victim = self.running.pop()
+        self.blocks.free(victim.block_ids)  # named blocks stay named: a readmission may find them again
+        victim.num_cached = 0
+        victim.num_named = 0
+        victim.num_preemptions += 1
         self.num_preemptions += 1
-        self.waiting.appendleft(req)
+        self.waiting.appendleft(victim)
+        return victim
+
+    # ------------------------------------------------------------------ leaving
 
     def finish(self, reqs: list[Request]) -> None:
+        """Finished or aborted running requests leave the running set and release their blocks."""
+        gone = set(map(id, reqs))
+        self.running = [r for r in self.running if id(r) not in gone]
         for req in reqs:
-            self.running.remove(req)
             self.blocks.free(req.block_ids)
 
     def remove_waiting(self, req_id: str) -> Request | None:
-        for req in self.waiting:
+        for i, req in enumerate(self.waiting):
             if req.req_id == req_id:
-                self.waiting.remove(req)
+                del self.waiting[i]
                 return req
         return None
