@@ -216,7 +216,9 @@ struct Mfma<F16> {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Reductions of lane l with lane l ^ 32 (v_permlane32_swap: the two halves of the wavefront exchange
-// values in the VALU, no LDS round trip).  Both lanes of a pair get the same bits.
+// values in the VALU, no LDS round trip) or with lane l ^ 16 (v_permlane16_swap: 16-lane rows 0 <-> 1
+// and 2 <-> 3).  Each swap returns the lane's own value and its partner's, in an order that depends on
+// the lane; max and + are commutative, so both lanes of a pair get the same bits.
 __device__ __forceinline__ float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -224,6 +226,21 @@ __device__ __forceinline__ float max_xor32(float x) {
 __device__ __forceinline__ float sum_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// NaN-propagating maxima (IEEE 754-2019 maximum: v_maximum3_f32, which needs no canonicalising moves on
+// values the compiler cannot prove quiet, unlike fmaxf's v_max_f32)
+__device__ __forceinline__ float maximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float maximum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float maximum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 constexpr float kLog2e = 1.4426950408889634f;

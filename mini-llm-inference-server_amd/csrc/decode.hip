@@ -99,14 +99,25 @@ __device__ __forceinline__ int qk_dim0(int kk, int g) {
   return F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : 32 * kk + 8 * g;
 }
 
-// Loads 16-token tile t of this wave's page range (lane (c, g); kbase/vbase: this head's bytes of the
-// pools, strides in bytes).
+// The next 16-token tile to load: its page within the split and its 16-token slice of that page (tiles
+// are loaded in order, once each, so a counter replaces a division by the tiles per page).
+struct LoadCursor {
+  int page = 0, sub = 0;
+  __device__ __forceinline__ void advance(int tpp) {
+    if (++sub == tpp) {
+      sub = 0;
+      ++page;
+    }
+  }
+};
+
+// Loads the 16-token tile at `at` of this wave's page range (lane (c, g); kbase/vbase: this head's bytes
+// of the pools, strides in bytes).
 template <bool F8, bool NT>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, const char* kbase, const char* vbase, int64_t tok_stride,
-                                          int64_t blk_stride, int page_lo, int page_hi, int t, int tpp, int c, int g,
+                                          int64_t blk_stride, int page_lo, int page_hi, LoadCursor at, int c, int g,
                                           TileRegs<F8>& r) {
-  const int page = t / tpp;
-  const int sub = t - page * tpp;
+  const int page = at.page, sub = at.sub;
   int blk = __builtin_amdgcn_readlane(page < 64 ? page_lo : page_hi, page & 63);
   if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
   const int64_t off = (int64_t)blk * blk_stride + (int64_t)(sub * 16) * tok_stride;
@@ -155,9 +166,8 @@ __device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4
       }
     }
   }
-  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  // the column's max over its four lanes l, l^16, l^32, l^48: two VALU swaps, no LDS round trip
+  const float mx = maximum_xor32(maximum_xor16(maximum(maximum(s[0], s[1]), maximum(s[2], s[3]))));
   if constexpr (kLazyRescale) {
     // the running max moves only when some column's tile max exceeds it by more than 2^8 (exp2 domain):
     // p then stays <= 256, which P and the fp32 accumulators hold as well as values below 1, and most
@@ -181,10 +191,7 @@ __device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_run);
-  float ps = (p[0] + p[1]) + (p[2] + p[3]);
-  ps += __shfl_xor(ps, 16, 64);
-  ps += __shfl_xor(ps, 32, 64);
-  l_run += ps;
+  l_run += sum_xor32(sum_xor16((p[0] + p[1]) + (p[2] + p[3])));
   const u32x2 pfrag = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
@@ -252,17 +259,23 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
 
   constexpr int R = PF + 1;
   TileRegs<F8> ring[R];
+  LoadCursor next;
 #pragma unroll
   for (int r = 0; r < PF; ++r)
-    if (r < ntiles) load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, r, tpp, c, g, ring[r]);
+    if (r < ntiles) {
+      load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[r]);
+      next.advance(tpp);
+    }
   for (int t0 = 0; t0 < ntiles; t0 += R) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int t = t0 + r;
       if (t < ntiles) {
-        if (t + PF < ntiles)
-          load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, t + PF, tpp, c, g,
+        if (t + PF < ntiles) {
+          load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g,
                             ring[(r + PF) % R]);
+          next.advance(tpp);
+        }
         if constexpr (F8) {
           u32x4 ka[4], va[4];
           widen<T>(ring[r], ka, va);
