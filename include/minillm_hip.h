@@ -136,7 +136,10 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  *      keys visible to the tile's last token, 64-key tiles they span} -> prefill_work[8 * num_prefill_work],
  *     across all rows in decreasing number of those tiles (the prefill kernel's work per item).
  * The caller computes the three counts from the same host facts (sequence lengths and new-token
- * counts); the kernel writes at most that many items.  pages_per_split <= 128.
+ * counts); the kernel writes at most that many items.  A decode item is written only when its partial
+ * slot (first_item + split) is below num_decode_work, and a merge item only when all of its row's slots
+ * are, so a step larger than the capacities loses those rows' work but never sends the decode or merge
+ * kernels past a workspace sized for num_decode_work items.  pages_per_split <= 128.
  */
 int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
               int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
@@ -147,8 +150,9 @@ int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t*
  * mllm_plan with the split size read from device memory at run time (*pages_per_split, clamped to
  * [min_pages_per_split, 128]).  No counterpart in the reference: it serves HIP-graph capture of decode steps
  * (the reference's planned M8, docs/distributed_inference_plan.md:309), where one captured plan launch
- * re-plans every replayed step.  The capacities must cover min_pages_per_split splits, so no item is ever
- * dropped; items past a step's own stay as the caller pre-filled them (-1).
+ * re-plans every replayed step.  The caller checks on the host that a staged step's items fit the
+ * capacities at the split size it stages (or runs that step without the graph), so no item is dropped;
+ * items past a step's own stay as the caller pre-filled them (-1).
  */
 int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
                   const int32_t* pages_per_split, int32_t min_pages_per_split, int32_t q_tile_tokens,

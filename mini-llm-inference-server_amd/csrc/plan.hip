@@ -122,12 +122,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
     int td, tm;
     const int od = base_d + wg_exclusive_scan(nd, sums, &td);
     const int om = base_m + wg_exclusive_scan(nm, sums, &tm);
+    // An item is emitted only when its position and its partial slot are inside the capacities, and a
+    // merge item only when every slot of its row is: a step larger than the caller sized for loses
+    // those rows' items instead of writing or reading partials past the workspace.
     for (int j = 0; j < nd; ++j) {
       const int sz = (int)(((int64_t)(j + 1) * pages) / nd - ((int64_t)j * pages) / nd);
       const int pos = atomicAdd(&offs[sz], 1);
-      if (pos < cap_decode) decode_work[pos] = make_int4(s, j, nd, od + j);
+      if (pos < cap_decode && od + j < cap_decode) decode_work[pos] = make_int4(s, j, nd, od + j);
     }
-    if (nm && om < cap_merge) merge_work[om] = make_int4(s, od, nd, 0);
+    if (nm && om < cap_merge && od + nd <= cap_decode) merge_work[om] = make_int4(s, od, nd, 0);
     if (pf) {  // {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: what the prefill kernel reads per item
       const int qs = qo_indptr[s], nn = qo_indptr[s + 1] - qs, cached = seq_lens[s] - nn, kv0 = kv_indptr[s];
       for (int t0 = 0; t0 < nn; t0 += q_tile) {

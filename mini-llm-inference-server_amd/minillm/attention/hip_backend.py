@@ -260,6 +260,8 @@ class HipBackend(AttentionBackend):
         g = h // hkv
         q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
         n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
+        if split_dev is not None:  # a captured step sized for fewer items than its worst case
+            n_dec = min(n_dec, meta.decode_items_cap)
         n_merge = sum(1 for p, nn in zip(pages, news) if nn == 1 and p > c)
         n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
         buf = torch.full((4 * n_dec + 4 * n_merge + 8 * n_pf,), -1, dtype=torch.int32, device=dev)

@@ -257,11 +257,17 @@ class StaticDecodeMetadata:
     them must cover.  The step's split-KV size is staged too (`meta.split_dev`, at least `meta.split_min`
     pages), so the captured plan splits each replayed step as an eager step of the same rows would."""
 
-    SPLIT_MIN = 8  # the smallest split the host heuristic picks: the plan's capacities are sized for it
+    SPLIT_MIN = 8  # the smallest split the host heuristic picks
 
-    def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int) -> None:
+    def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int,
+                 decode_items: int | None = None) -> None:
+        """`decode_items` caps the plan's split-KV items (default: every row at `max_blocks` blocks in
+        splits of SPLIT_MIN pages); a step whose items at its staged split size exceed it must not be
+        staged (see items())."""
         self.num_rows, self.tables, self.block_size = num_rows, tables, block_size
         self.max_blocks = tables.max_blocks
+        worst = num_rows * -(-self.max_blocks // self.SPLIT_MIN)
+        self.decode_items = worst if decode_items is None else max(num_rows, min(worst, int(decode_items)))
         dev = tables.device
         # num_cached | num_new | rows | num_blocks | split size | table updates (at most every entry of B rows)
         self._upd = 4 * num_rows + 1
@@ -273,6 +279,18 @@ class StaticDecodeMetadata:
                                               num_rows * self.max_blocks, dev)
         self.meta.split_dev = self.packed[4 * num_rows:4 * num_rows + 1]
         self.meta.split_min = self.SPLIT_MIN
+        self.meta.decode_items_cap = self.decode_items
+
+    def split_size(self, pages_per_split: int) -> int:
+        """The split size a staged step runs with (what mllm_plan_dev clamps it to)."""
+        return max(self.SPLIT_MIN, min(128, int(pages_per_split)))
+
+    def items(self, seqs: list[SeqStep], pages_per_split: int) -> int:
+        """Split-KV items of the step at its staged split size, padding rows included (one page each)."""
+        c = self.split_size(pages_per_split)
+        bs = self.block_size
+        pages = [-(-(s.num_cached + 1) // bs) for s in seqs]
+        return sum(-(-p // c) for p in pages) + (self.num_rows - len(seqs))
 
     def load(self, keys, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
         """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host packing,
@@ -299,7 +317,7 @@ class StaticDecodeMetadata:
         host[2 * b + n:3 * b] = self.tables.pad_row
         host[3 * b:3 * b + n] = [len(s.block_ids) for s in seqs]
         host[3 * b + n:4 * b] = 1
-        host[4 * b] = max(self.SPLIT_MIN, min(128, int(pages_per_split)))
+        host[4 * b] = self.split_size(pages_per_split)
         u = len(updates)
         host[self._upd:self._upd + u] = updates
         end = self._upd + u

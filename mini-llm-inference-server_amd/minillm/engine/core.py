@@ -224,7 +224,7 @@ class EngineCore:
         reqs = [r for r, _ in rows]
         new = [r.uncached()[:n] for r, n in rows]
         seqs = [SeqStep(r.num_cached, len(t), r.block_ids) for r, t in zip(reqs, new)]
-        if decode_only and self.graphs is not None and self.graphs.supports(len(seqs)):
+        if decode_only and self.graphs is not None and self.graphs.fits(seqs):
             logits, greedy = self.graphs.run(reqs, seqs, [t[0] for t in new])
         else:
             meta = self.tables.build(reqs, seqs, BLOCK_SIZE) if self.tables is not None \

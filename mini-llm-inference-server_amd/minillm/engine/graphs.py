@@ -11,12 +11,15 @@ after the scheduler has picked its rows into one HIP graph over fixed device buf
 A step then costs the host one packed upload of (num_cached, num_new, block tables), one input-id copy,
 one graph launch and the read of B token ids.
 
-The graph is captured with worst-case sizes: every row may hold up to ceil(max_model_len / block_size)
-blocks, so the plan's capacities cover B rows at that length split into the smallest splits, and the
-plan slots a step leaves unused stay -1, which every kernel skips.  Each replay stages the split size
-an eager step of the same rows would use (mllm_plan_dev reads it on the device), so a replayed step
-runs the same decode work as the eager one.  Rows past the step's own are padding (see
-StaticDecodeMetadata).
+The graph is captured with fixed sizes.  A row may hold up to ceil(max_model_len / block_size) blocks;
+the plan's split-KV capacity of a B-row bucket is the smaller of B rows at that length in the smallest
+splits and the whole pool in the smallest splits plus one item per row (without prefix sharing, a step's
+pages never exceed the pool).  Each replay stages the split size an eager step of the same rows would
+use (mllm_plan_dev reads it on the device), so a replayed step runs the same decode work as the eager
+one; a step whose items at that size exceed the bucket's capacity (rows sharing prefix pages can) is
+not replayed but run eagerly (`fits`).  The plan slots a step leaves unused stay -1, which every kernel
+skips.  Rows past the step's own are padding (see StaticDecodeMetadata).  All buckets share one decode
+workspace, sized for the largest: replays run one at a time on the engine's stream.
 Only pure decode steps run as graphs; prefill and mixed steps run eagerly.
 """
 
@@ -51,9 +54,13 @@ class DecodeGraphs:
         self.buckets = tuple(sorted(set(int(b) for b in buckets)))
         self.device = next(model.parameters()).device
         self.num_kv_heads = model.config.num_key_value_heads
+        self.num_heads = model.config.num_attention_heads
+        self.head_dim = model.config.head_dim
         self._captured: dict[int, _Captured] = {}
         self._pool = None
+        self._workspace: torch.Tensor | None = None  # shared by every bucket's graph
         self.replays = 0
+        self.eager_fallbacks = 0
         self.last_bucket: int | None = None
 
     def supports(self, num_rows: int) -> bool:
@@ -61,6 +68,26 @@ class DecodeGraphs:
 
     def bucket(self, num_rows: int) -> int:
         return next(b for b in self.buckets if b >= num_rows)
+
+    def capacity(self, bucket: int) -> int:
+        """Split-KV items the bucket's plan holds."""
+        c = StaticDecodeMetadata.SPLIT_MIN
+        worst = bucket * -(-self.tables.max_blocks // c)
+        return min(worst, -(-self.cache.num_blocks // c) + bucket)
+
+    def fits(self, seqs: list[SeqStep]) -> bool:
+        """Whether the decode step `seqs` can replay a graph: a bucket holds its rows, and its split-KV
+        items at the split size it would stage fit that bucket's plan."""
+        if not self.supports(len(seqs)):
+            return False
+        b = self.bucket(len(seqs))
+        pages = [-(-(s.num_cached + 1) // self.block_size) for s in seqs]
+        c = max(StaticDecodeMetadata.SPLIT_MIN, min(128, pages_per_split(sum(pages), self.num_kv_heads)))
+        items = sum(-(-p // c) for p in pages) + (b - len(seqs))
+        if items <= self.capacity(b):
+            return True
+        self.eager_fallbacks += 1
+        return False
 
     def run(self, keys, seqs: list[SeqStep], token_ids: list[int]) -> tuple[torch.Tensor, torch.Tensor]:
         """One decode step: `seqs` are the rows (one new token each, its id in `token_ids`), `keys` their
@@ -101,12 +128,17 @@ class DecodeGraphs:
 
     @torch.inference_mode()
     def _capture(self, bucket: int) -> _Captured:
-        static = StaticDecodeMetadata(bucket, self.tables, self.block_size)
+        static = StaticDecodeMetadata(bucket, self.tables, self.block_size, decode_items=self.capacity(bucket))
         c = _Captured(static, torch.zeros((1, bucket), dtype=torch.long, device=self.device),
                       torch.zeros(bucket, dtype=torch.long, pin_memory=True))
         self._stage(c, [], [], [])  # every row padding: a valid step that writes nothing to the pool
-        # warm-up on a side stream (sizes a fresh workspace for the worst-case plan), then capture
-        self.backend.detach_workspace()
+        if self._workspace is None:  # sized for the largest bucket's plan: no bucket ever grows it
+            nbytes = self.backend._lib.workspace_bytes(self.capacity(self.buckets[-1]), self.num_heads,
+                                                       self.head_dim)
+            self._workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        # warm-up on a side stream, then capture, with the shared workspace in the backend
+        eager_ws = self.backend.detach_workspace()
+        self.backend._workspace = self._workspace
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
@@ -119,7 +151,10 @@ class DecodeGraphs:
             self._pool = torch.cuda.graph_pool_handle()
         with torch.cuda.graph(c.graph, pool=self._pool):
             c.logits, c.tokens = self._body(c)
-        c.workspace = self.backend.detach_workspace()  # owned by the graph from now on
+        if self.backend.detach_workspace() is not self._workspace:
+            raise RuntimeError("the decode workspace was reallocated during capture")
+        c.workspace = self._workspace
+        self.backend._workspace = eager_ws
         self.backend.invalidate_plan()  # eager steps must not reuse the captured plan buffers
         torch.cuda.synchronize(self.device)
         return c

@@ -41,12 +41,17 @@ def run_engine(model, backend, builder, ps, max_tokens, **kw):
     for i, p in enumerate(ps):
         core.add_request(AddRequest(f"r{i}", p, max_tokens))
     last = {}
-    hook = model.register_forward_hook(lambda mod, args, out: last.__setitem__("logits", out))
+    hook = model.register_forward_hook(lambda mod, args, out: last.__setitem__("logits", out[:, -1]))
     outs = {}
+    replays = 0
     try:
         while core.has_work():
             step = core.step()
-            logits = last["logits"][:, -1]
+            logits = last["logits"]
+            if core.graphs is not None and core.graphs.replays > replays:  # the step replayed a graph: no hook
+                replays = core.graphs.replays
+                logits = core.graphs.captured(core.graphs.last_bucket).logits[:len(step.outputs)]
+            assert logits.shape[0] == len(step.outputs)
             top2 = logits.float().topk(2, dim=-1).values
             # the margin in units of the logits' own rounding step at the top logit
             ulp = torch.finfo(logits.dtype).eps * top2[:, 0].abs().clamp_min(1.0)

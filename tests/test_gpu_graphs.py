@@ -1,6 +1,7 @@
 """Decode steps as captured HIP graphs (DecodeGraphs): every replay equals the same step run eagerly, bit
-for bit, with eager steps (prefills, other buckets) and synchronisations between replays; and the engine
-with graphs gives the eager engine's greedy tokens, on bf16 and fp8 pools."""
+for bit, with eager steps (prefills, other buckets) and synchronisations between replays; the engine
+with graphs gives the eager engine's greedy tokens, on bf16 and fp8 pools, also when steps exceed a
+bucket's plan capacity and run eagerly; and it gives the oracle engine's greedy tokens."""
 
 import pytest
 import torch
@@ -70,3 +71,39 @@ def test_graph_rejects_what_it_cannot_hold(hip):
         sm.load([0], [SeqStep(0, 2, [1])])
     with pytest.raises(ValueError, match="exceeds"):
         sm.load([0], [SeqStep(200, 1, list(range(13)))])
+
+
+def test_graph_steps_beyond_the_plan_capacity_run_eagerly(hip):
+    # a bucket's split-KV capacity is sized from the pool; rows sharing a long prompt head (prefix cache)
+    # reference more pages than the pool holds, so those steps fall back to eager launches, while the
+    # steps that fit still replay; tokens equal the eager engine's either way
+    from minillm.attention import get_backend
+    from minillm.attention.metadata import AttentionMetadata
+
+    model = tiny_model(seed=61)
+    head = prompts(1, 300, 301, seed=62)[0]
+    ps = [head + p for p in prompts(8, 1, 12, seed=63)]
+    kw = dict(max_batch_size=8, num_kv_blocks=40, max_model_len=2048)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 40, decode_graphs=True, **kw)
+    exp, _ = run_engine(model, get_backend("hip"), AttentionMetadata.build, ps, 40, **kw)
+    assert_greedy_match(got, exp)
+    g = core.graphs
+    assert g.eager_fallbacks > 0 and g.replays > 0
+    assert g.capacity(8) < 8 * -(-core.tables.max_blocks // 8)  # sized from the pool, not max_model_len
+    assert core.stats().prefix_cache_hits > 0
+
+
+def test_graph_engine_matches_oracle_engine(hip):
+    # decode steps replayed from graphs against the oracle engine (metadata and attention from the oracle,
+    # float32), greedy; tests/test_gpu_engine_8b.py compares them teacher-forced at the 8B shape
+    from oracle_engine import OracleBackend, oracle_metadata
+
+    from minillm.attention import get_backend
+
+    model = tiny_model(seed=71)
+    ps = prompts(10, 1, 300, seed=72)
+    kw = dict(max_batch_size=8, num_kv_blocks=300, max_model_len=2048)
+    got, core = run_engine(model, get_backend("hip"), None, ps, 24, decode_graphs=True, **kw)
+    exp, _ = run_engine(model, OracleBackend(), oracle_metadata, ps, 24, **kw)
+    assert_greedy_match(got, exp)
+    assert core.graphs.replays > 10
