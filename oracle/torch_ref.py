@@ -115,14 +115,35 @@ def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torc
     return tokens.transpose(1, 2)
 
 
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Tensor | None = None,
+         is_causal: bool = False, p_round: torch.dtype | None = None) -> torch.Tensor:
+    """`F.scaled_dot_product_attention(..., enable_gqa=True)` (scale 1/sqrt(Dh), bottom-right causal
+    when `is_causal`: the reference only sets it when Tq == Tk).  With `p_round`, the same mathematics
+    written out in q's dtype, with the softmax probabilities rounded to `p_round` before the product with
+    V, which is how flash-style bf16 kernels form P.  That variant is not the reference's computation:
+    it is the noise-floor reference of bf16 attention arithmetic for end-to-end comparisons."""
+    if p_round is None:
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal, enable_gqa=True)
+    g = q.shape[1] // k.shape[1]
+    k, v = k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1)
+    s = torch.matmul(q, k.transpose(-2, -1)) * (q.shape[-1] ** -0.5)
+    tq, tk = s.shape[-2:]
+    if is_causal:
+        attn_mask = torch.ones(tq, tk, dtype=torch.bool, device=q.device).tril(diagonal=tk - tq)
+    if attn_mask is not None:
+        s = s.masked_fill(~attn_mask, -math.inf)
+    p = torch.softmax(s, dim=-1).to(p_round).to(s.dtype)
+    return torch.matmul(p, v)
+
+
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
                     compute_dtype: torch.dtype | None = None, k_scale: float = 1.0,
-                    v_scale: float = 1.0) -> torch.Tensor:
+                    v_scale: float = 1.0, p_round: torch.dtype | None = None) -> torch.Tensor:
     """Reference `paged_torch_ref.py:40-74`.  q [N, H, Dh] -> [N, H, Dh]; the step's own k/v must
     already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`.  With `compute_dtype` the
     gathered context and q are converted to it before SDPA (and the result back to q's dtype): how the
     oracle runs on a GPU, in float32.  An fp8 pool's gathered rows are dequantized (value * scale, in
-    `compute_dtype` or q's dtype)."""
+    `compute_dtype` or q's dtype).  `p_round` selects the rounded-P variant of `sdpa`."""
     if getattr(k_cache, "dtype", None) == FP8:
         cd = compute_dtype or q.dtype
 
@@ -130,7 +151,8 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
             return lambda t: dequantize_fp8(t.view(FP8), scale, cd)
 
         kb, vb = k_cache.view(torch.uint8), v_cache.view(torch.uint8)  # gathered as bytes (no float8 indexing)
-        out = paged_attention(q.to(cd), _Converted(kb, deq(k_scale)), _Converted(vb, deq(v_scale)), meta)
+        out = paged_attention(q.to(cd), _Converted(kb, deq(k_scale)), _Converted(vb, deq(v_scale)), meta,
+                              p_round=p_round)
         return out.to(q.dtype)
     if compute_dtype is not None and compute_dtype != q.dtype:
         orig = q.dtype
@@ -138,7 +160,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         def conv(t):
             return t.to(compute_dtype)
 
-        out = paged_attention(conv(q), _Converted(k_cache, conv), _Converted(v_cache, conv), meta)
+        out = paged_attention(conv(q), _Converted(k_cache, conv), _Converted(v_cache, conv), meta, p_round=p_round)
         return out.to(orig)
     out = torch.empty_like(q)
     starts, lens, news = meta.query_start_loc, meta.seq_lens, meta.num_new
@@ -155,7 +177,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         if any(lens[i] != longest for i in decode):
             ends = torch.tensor([lens[i] for i in decode], device=q.device)
             mask = (torch.arange(longest, device=q.device)[None, :] < ends[:, None])[:, None, None, :]
-        out[token_idx] = F.scaled_dot_product_attention(qd, k, v, attn_mask=mask, enable_gqa=True)[:, :, 0]
+        out[token_idx] = sdpa(qd, k, v, attn_mask=mask, p_round=p_round)[:, :, 0]
 
     for i, n in enumerate(news):
         if n == 1:
@@ -165,10 +187,10 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         v = gather(v_cache, meta.block_tables[i:i + 1], length)
         qi = q[s:s + n].transpose(0, 1)[None]
         if n == length:
-            o = F.scaled_dot_product_attention(qi, k, v, is_causal=True, enable_gqa=True)
+            o = sdpa(qi, k, v, is_causal=True, p_round=p_round)
         else:
             mask = torch.ones(n, length, dtype=torch.bool, device=q.device).tril(diagonal=length - n)
-            o = F.scaled_dot_product_attention(qi, k, v, attn_mask=mask, enable_gqa=True)
+            o = sdpa(qi, k, v, attn_mask=mask, p_round=p_round)
         out[s:s + n] = o[0].transpose(0, 1)
     return out
 

@@ -21,17 +21,20 @@ def oracle_metadata(seqs, block_size, device):
 
 
 class OracleBackend:
-    """write_kv + gather/SDPA restated from the reference; attention computed in float32."""
+    """write_kv + gather/SDPA restated from the reference; attention computed in float32.  With
+    `p_round` (torch.bfloat16) the softmax probabilities are rounded before the product with V: bf16
+    attention arithmetic, the noise-floor reference of end-to-end comparisons."""
 
     name = "oracle"
 
-    def __init__(self, compute_dtype=torch.float32) -> None:
+    def __init__(self, compute_dtype=torch.float32, p_round=None) -> None:
         self.compute_dtype = compute_dtype
+        self.p_round = p_round
 
     def forward(self, q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
         torch_ref.write_kv(k_cache, v_cache, meta.slot_mapping, k, v, k_scale, v_scale)
         return torch_ref.paged_attention(q, k_cache, v_cache, meta, compute_dtype=self.compute_dtype,
-                                         k_scale=k_scale, v_scale=v_scale)
+                                         k_scale=k_scale, v_scale=v_scale, p_round=self.p_round)
 
     def prefill(self, q, k, v, key_valid=None, **kwargs):
         dt = q.dtype

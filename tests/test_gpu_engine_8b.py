@@ -1,0 +1,189 @@
+"""The end-to-end engine at Llama-3.1-8B's full shape on the GPU: the HIP hot path against the oracle's,
+teacher-forced, over every sampled position (the reference's G1b: src/minillm/correctness.py:34-83,
+docs/decisions/04-correctness.md:22-29).
+
+Workload, the full end-to-end configuration: 32 layers, hidden 4096, 32 query / 8 KV heads, head_dim
+128, FFN 14336, vocab 128256, bf16 weights ~ N(0, 0.02) (seed 0); 128 requests with prompts of
+U[256, 2048] random token ids, 256 greedy tokens each; 16-token blocks, the pool sized for 90% occupancy;
+continuous batching, prefill-first, no prefix caching.  The full 128 x 256 = 32,768 positions are compared.
+
+1. The HIP engine runs greedily; the logits of every sampled position are kept (bf16, on the GPU).
+2. The oracle engine (metadata and attention from the oracle, attention in float32) runs the same
+   requests with its sampler forced to the HIP engine's tokens: the scheduler then takes the same steps
+   over the same tokens, so every position has logits from both.  Drift(oracle, HIP): mean KL(oracle ||
+   HIP), max |dlogit|, and top-1 flips where the oracle's top-1/top-2 margin exceeds 0.5 logit.
+3. The noise floor: the oracle engine again, with its softmax probabilities rounded to bf16 before the
+   product with V (bf16 attention arithmetic), forced to the same tokens, against step 2's logits.
+4. The HIP engine with its decode steps replayed as captured HIP graphs, forced to the same tokens,
+   against step 2's logits.
+Pass, for steps 1 and 4: no clear-margin flip, and mean KL and max |dlogit| within 2x the noise floor's
+(with the reference's floors 1e-5 and 0.125, correctness.py:25-28).  The greedy comparison is logged
+too: positions where the HIP engine's greedy token is not the oracle's argmax, and the largest oracle
+margin among them.
+"""
+
+import sys
+import time
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle_engine import OracleBackend, oracle_metadata
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+REQUESTS, STEPS = 128, 256
+MARGIN, KL_FLOOR, DIFF_FLOOR = 0.5, 1e-5, 0.125
+
+
+_CAPSYS = []  # the running test's capsys: progress lines bypass pytest's output capture
+
+
+def progress(msg: str) -> None:
+    """A line on the real terminal as the work goes (the test runs for minutes)."""
+    if _CAPSYS:
+        with _CAPSYS[0].disabled():
+            print(f"[engine_8b] {msg}", flush=True)
+    else:
+        print(f"[engine_8b] {msg}", file=sys.stderr, flush=True)
+
+
+class Drift:
+    """Per-position comparison of a test run's logits with a reference run's (reference
+    correctness.py:55-69), accumulated over steps on the GPU."""
+
+    def __init__(self) -> None:
+        self.kl_sum = torch.zeros((), dtype=torch.float64, device=DEV)
+        self.max_diff = torch.zeros((), device=DEV)
+        self.flips = torch.zeros((), dtype=torch.long, device=DEV)
+        self.differ = torch.zeros((), dtype=torch.long, device=DEV)
+        self.max_margin_differ = torch.zeros((), device=DEV)
+        self.positions = 0
+
+    def add(self, ref: torch.Tensor, tst: torch.Tensor) -> None:
+        ref, tst = ref.float(), tst.float()
+        lp_r, lp_t = F.log_softmax(ref, -1), F.log_softmax(tst, -1)
+        self.kl_sum += (lp_r.exp() * (lp_r - lp_t)).sum(-1).double().sum()
+        self.max_diff = torch.maximum(self.max_diff, (ref - tst).abs().max())
+        top2 = ref.topk(2, dim=-1).values
+        margin = top2[:, 0] - top2[:, 1]
+        differ = ref.argmax(-1) != tst.argmax(-1)
+        self.flips += (differ & (margin > MARGIN)).sum()
+        self.differ += differ.sum()
+        self.max_margin_differ = torch.maximum(self.max_margin_differ, torch.where(differ, margin, 0.0).max())
+        self.positions += ref.shape[0]
+
+    def summary(self) -> dict:
+        return {"positions": self.positions, "mean_kl": self.kl_sum.item() / max(1, self.positions),
+                "max_abs_diff": self.max_diff.item(), "clear_margin_flips": int(self.flips.item()),
+                "argmax_differs": int(self.differ.item()), "max_margin_where_differs": self.max_margin_differ.item()}
+
+
+@pytest.fixture(scope="module")
+def llama8b():
+    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
+    from minillm.model.llama import LlamaForCausalLM, random_init_
+
+    cfg = LlamaConfig(**LLAMA_3_1_8B)
+    with torch.device("meta"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to_empty(device=DEV).to(torch.bfloat16)
+    random_init_(model, std=0.02, seed=0)
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(256, 2049, (REQUESTS,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
+    blocks = -(-sum(-(-(n + STEPS) // 16) for n in lens) * 10 // 9)
+    yield model, prompts, blocks
+    del model
+    torch.cuda.empty_cache()
+
+
+def run_engine(model, backend, builder, prompts, blocks, sampler, label, **kw):
+    from minillm.engine.core import AddRequest, EngineCore
+
+    model.set_backend(backend)
+    core = EngineCore(model, max_model_len=4096, max_batch_size=REQUESTS, num_kv_blocks=blocks,
+                      enable_prefix_caching=False, metadata_builder=builder, sampler=sampler, step_log=True, **kw)
+    for i, p in enumerate(prompts):
+        core.add_request(AddRequest(f"r{i}", p, STEPS, ignore_eos=True))
+    t0 = time.perf_counter()
+    out = {}
+    while core.has_work():
+        for o in core.step().outputs:
+            out.setdefault(o.req_id, []).extend(o.new_token_ids)
+        if len(core.step_log) % 32 == 0:
+            progress(f"{label}: step {len(core.step_log)}, {time.perf_counter() - t0:.0f} s")
+    st = core.stats()
+    info = {"steps": len(core.step_log), "seconds": round(time.perf_counter() - t0, 1),
+            "preemptions": st.num_preemptions, "graph_replays": core.graphs.replays if core.graphs else 0}
+    progress(f"{label}: done, {info}")
+    del core
+    torch.cuda.empty_cache()
+    return out, info
+
+
+def _rows(reqs):
+    idx = torch.tensor([int(r.req_id[1:]) for r in reqs], device=DEV)
+    pos = torch.tensor([len(r.output) for r in reqs], device=DEV)
+    return idx, pos
+
+
+def test_engine_8b_teacher_forced_against_oracle(hip, llama8b, capsys):
+    from minillm.attention import get_backend
+
+    _CAPSYS[:] = [capsys]
+
+    model, prompts, blocks = llama8b
+    vocab = model.config.vocab_size
+    with torch.inference_mode():
+        hip_logits = torch.empty((REQUESTS, STEPS, vocab), dtype=torch.bfloat16, device=DEV)
+        ref_logits = torch.empty_like(hip_logits)
+
+    # 1. the HIP engine, greedy, every position's logits kept
+    def greedy_kept(reqs, logits):
+        idx, pos = _rows(reqs)
+        hip_logits[idx, pos] = logits
+        return logits.argmax(dim=-1).tolist()
+
+    tokens, hip_info = run_engine(model, get_backend("hip"), None, prompts, blocks, greedy_kept, "hip greedy")
+    assert all(len(tokens[f"r{i}"]) == STEPS for i in range(REQUESTS))
+
+    def forced(store=None, drift=None, against=None):
+        def sample(reqs, logits):
+            idx, pos = _rows(reqs)
+            if store is not None:
+                store[idx, pos] = logits
+            if drift is not None:
+                ref, tst = (logits, against[idx, pos]) if store is not None else (against[idx, pos], logits)
+                drift.add(ref, tst)
+            return [tokens[r.req_id][len(r.output)] for r in reqs]
+        return sample
+
+    # 2. the oracle engine forced to those tokens: the reference logits, and the HIP engine's drift from them
+    ours = Drift()
+    _, oracle_info = run_engine(model, OracleBackend(), oracle_metadata, prompts, blocks,
+                                forced(store=ref_logits, drift=ours, against=hip_logits), "oracle fp32")
+    # 3. the noise floor: bf16 attention arithmetic in the oracle
+    noise = Drift()
+    _, noise_info = run_engine(model, OracleBackend(p_round=torch.bfloat16), oracle_metadata, prompts, blocks,
+                               forced(drift=noise, against=ref_logits), "oracle bf16-P")
+    # 4. the HIP engine with decode steps as captured HIP graphs
+    graphs = Drift()
+    _, graph_info = run_engine(model, get_backend("hip"), None, prompts, blocks,
+                               forced(drift=graphs, against=ref_logits), "hip graphs", decode_graphs=True)
+
+    n, o, g = noise.summary(), ours.summary(), graphs.summary()
+    kl_limit = 2 * max(n["mean_kl"], KL_FLOOR)
+    diff_limit = 2 * max(n["max_abs_diff"], DIFF_FLOOR)
+    progress(f"runs: hip {hip_info}, oracle {oracle_info}, noise {noise_info}, graphs {graph_info}")
+    progress(f"noise floor (oracle bf16-P vs fp32): {n}")
+    progress(f"hip eager vs oracle: {o}")
+    progress(f"hip graphs vs oracle: {g}")
+    progress(f"limits: mean KL <= {kl_limit:.3e}, max |dlogit| <= {diff_limit:.4f}")
+    assert o["positions"] == n["positions"] == g["positions"] == REQUESTS * STEPS
+    assert graph_info["graph_replays"] > 0
+    for name, d in (("eager", o), ("graphs", g)):
+        assert d["clear_margin_flips"] == 0, f"{name}: top-1 differs where the oracle leads by > {MARGIN}: {d}"
+        assert d["mean_kl"] <= kl_limit, f"{name}: mean KL {d['mean_kl']:.3e} > {kl_limit:.3e}"
+        assert d["max_abs_diff"] <= diff_limit, f"{name}: max |dlogit| {d['max_abs_diff']:.4f} > {diff_limit:.4f}"

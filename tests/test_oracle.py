@@ -199,6 +199,39 @@ def test_paged_attention_bf16_kernel_case_close_to_textbook():
         torch.testing.assert_close(out[st:st + n].double(), exp.transpose(0, 1), atol=2e-2, rtol=1e-2)
 
 
+def _kernel_case_step():
+    case = cases()["kernel_mixed_step"]  # decode rows, a fresh prompt and a prompt over cached tokens
+    q, k, v, pool_k, pool_v, meta, seqs, ctx_k, ctx_v = build_step(case)
+    tm = torch_ref.torch_meta(meta, "cpu")
+    torch_ref.write_kv(pool_k, pool_v, tm.slot_mapping, k, v)
+    return q, pool_k, pool_v, tm, meta, seqs, ctx_k, ctx_v
+
+
+def test_rounded_p_variant_without_rounding_is_sdpa():
+    # the written-out attention of the noise-floor variant, with a rounding that changes nothing (float32
+    # probabilities stay float32), equals the library SDPA path and the float64 textbook on every row kind
+    q, pool_k, pool_v, tm, meta, seqs, ctx_k, ctx_v = _kernel_case_step()
+    lib = torch_ref.paged_attention(q, pool_k, pool_v, tm)
+    explicit = torch_ref.paged_attention(q, pool_k, pool_v, tm, p_round=torch.float32)
+    torch.testing.assert_close(explicit, lib, atol=2e-6, rtol=1e-5)
+    for i, s in enumerate(seqs):
+        st, n, length = meta.query_start_loc[i], s.num_new, meta.seq_lens[i]
+        exp = naive_attention(q[st:st + n].transpose(0, 1), ctx_k[i].transpose(0, 1), ctx_v[i].transpose(0, 1),
+                              causal_allowed(n, length))
+        torch.testing.assert_close(explicit[st:st + n].double(), exp.transpose(0, 1), atol=1e-5, rtol=1e-5)
+
+
+def test_rounded_p_variant_moves_outputs_by_at_most_the_bf16_rounding_of_p():
+    # rounding each probability to bf16 (relative error <= 2^-9) moves an output by at most
+    # 2^-9 * sum_j p_j |v_j| <= 2^-9 * max |v|, and it does move them
+    q, pool_k, pool_v, tm, meta, seqs, ctx_k, ctx_v = _kernel_case_step()
+    exact = torch_ref.paged_attention(q, pool_k, pool_v, tm)
+    rounded = torch_ref.paged_attention(q, pool_k, pool_v, tm, p_round=torch.bfloat16)
+    vmax = max(v.abs().max().item() for v in ctx_v)
+    diff = (rounded - exact).abs().max().item()
+    assert 0 < diff <= 2 ** -9 * vmax + 1e-5
+
+
 # ---------------------------------------------------------------- contiguous prefill
 
 
