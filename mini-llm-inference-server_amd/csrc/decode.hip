@@ -373,14 +373,16 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
 constexpr int kPrefetch = MLLM_DECODE_PREFETCH;
 constexpr bool kNonTemporal = true;
 constexpr int kOccupancy = MLLM_DECODE_OCC;
-// fp8 tiles hold half the bytes in half the registers: three tiles of lookahead (154 VGPRs, no spill)
-// measured 213-215 us on decode_256 against 219-226 us with two.
+// fp8 tiles hold half the bytes in half the registers, and widening them adds VALU work per byte: four
+// tiles of lookahead at 2 wavefronts per SIMD (171 VGPRs, no spill) measured 198.3-198.7 us on
+// decode_256 (5.62-5.63 TB/s), against 203-204 us for 3 tiles at 3 per SIMD, 205 us for 1 at 4 and
+// 213 us for 2 at 3 (same box, alternating); 5 and 6 tiles at 2 per SIMD match 4, 8 is 1% slower.
 #ifndef MLLM_DECODE_FP8_PREFETCH
-#define MLLM_DECODE_FP8_PREFETCH 3
+#define MLLM_DECODE_FP8_PREFETCH 4
 #endif
 constexpr int kPrefetchFp8 = MLLM_DECODE_FP8_PREFETCH;
 #ifndef MLLM_DECODE_FP8_OCC
-#define MLLM_DECODE_FP8_OCC 3
+#define MLLM_DECODE_FP8_OCC 2
 #endif
 constexpr int kOccupancyFp8 = MLLM_DECODE_FP8_OCC;
 
