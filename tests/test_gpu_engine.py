@@ -33,34 +33,31 @@ def prompts(n, lo, hi, seed, vocab=256):
 
 
 def run_engine(model, backend, builder, ps, max_tokens, **kw):
-    """Runs the engine to completion; returns {req_id: [(token, top1 - top2 margin in logit ulps), ...]}."""
+    """Runs the engine to completion; returns {req_id: [(token, top1 - top2 margin in logit ulps), ...]}.
+    Tokens are the greedy argmax of each row's logits, picked by a sampler that also records the row's
+    margin under its request id (rows and logits arrive together, also for steps replayed from graphs and
+    for chunk rows that sample nothing)."""
     from minillm.engine.core import AddRequest, EngineCore
 
+    margin = {}
+
+    def greedy(reqs, logits):
+        top2 = logits.float().topk(2, dim=-1).values
+        # the margin in units of the logits' own rounding step at the top logit
+        ulp = torch.finfo(logits.dtype).eps * top2[:, 0].abs().clamp_min(1.0)
+        for r, m in zip(reqs, ((top2[:, 0] - top2[:, 1]) / ulp).tolist()):
+            margin[r.req_id] = m
+        return logits.argmax(dim=-1).tolist()
+
     model.set_backend(backend)
-    core = EngineCore(model, metadata_builder=builder, **kw)
+    core = EngineCore(model, metadata_builder=builder, sampler=greedy, **kw)
     for i, p in enumerate(ps):
         core.add_request(AddRequest(f"r{i}", p, max_tokens))
-    last = {}
-    hook = model.register_forward_hook(lambda mod, args, out: last.__setitem__("logits", out[:, -1]))
     outs = {}
-    replays = 0
-    try:
-        while core.has_work():
-            step = core.step()
-            logits = last["logits"]
-            if core.graphs is not None and core.graphs.replays > replays:  # the step replayed a graph: no hook
-                replays = core.graphs.replays
-                logits = core.graphs.captured(core.graphs.last_bucket).logits[:len(step.outputs)]
-            assert logits.shape[0] == len(step.outputs)
-            top2 = logits.float().topk(2, dim=-1).values
-            # the margin in units of the logits' own rounding step at the top logit
-            ulp = torch.finfo(logits.dtype).eps * top2[:, 0].abs().clamp_min(1.0)
-            margins = ((top2[:, 0] - top2[:, 1]) / ulp).tolist()
-            for o, m in zip(step.outputs, margins):
-                outs.setdefault(o.req_id, []).extend((t, m) for t in o.new_token_ids)
-            core.check_blocks()
-    finally:
-        hook.remove()
+    while core.has_work():
+        for o in core.step().outputs:
+            outs.setdefault(o.req_id, []).extend((t, margin[o.req_id]) for t in o.new_token_ids)
+        core.check_blocks()
     return outs, core
 
 
