@@ -19,7 +19,9 @@ workloads on the GPU with their own kernels' rates and the same CPU baseline:
   mixed_128   8 prefill + 120 decode rows: prefill launch TFLOP/s and fraction of the bf16 peak over
               its own launch, decode launch GB/s, and the step with both launches overlapped;
   prefix_64   64 rows over a shared 2,048-token prefix: prefill launch TFLOP/s and fraction;
-  decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction.
+  decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction;
+  engine_8b   the end-to-end engine on a random-init Llama-3.1-8B, 128 requests x 256 greedy tokens:
+              decode tokens/s over its decode steps.
 
     python bench.py [--steps K] [--warmup W] [--workload decode_256|decode_4|mixed_128|prefix_64]
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
@@ -174,63 +176,91 @@ def rotary_append_times(wl, backend, meta, q, k, v, pool_k, pool_v, reps=20):
     return out
 
 
+def engine_8b_model(requests: int, decode_steps: int):
+    """A random-init Llama-3.1-8B (bf16 weights ~ N(0, 0.02), seed 0) on cuda:0, `requests` prompts of
+    U[256, 2048] random tokens (seed 0), and the pool size for 90% occupancy with `decode_steps` tokens
+    each: (model, prompts, blocks)."""
+    import torch
+
+    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
+    from minillm.model.llama import LlamaForCausalLM, random_init_
+
+    cfg = LlamaConfig(**LLAMA_3_1_8B)
+    with torch.device("meta"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to_empty(device=torch.device("cuda:0")).to(torch.bfloat16)
+    random_init_(model, std=0.02, seed=0)
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(256, 2049, (requests,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
+    blocks = -(-sum(-(-(n + decode_steps) // 16) for n in lens) * 10 // 9)
+    return model, prompts, blocks
+
+
+def engine_run(model, prompts, blocks, backend, builder, decode_steps: int, chunked_prefill: bool = False,
+               max_num_batched_tokens: int = 8192, kv_fp8: bool = False, decode_graphs: bool = False,
+               record_margins: bool = False):
+    """Every prompt through the engine (continuous batching, 16-token blocks, greedy, ignore EOS) until each
+    has `decode_steps` tokens; returns ({req_id: tokens}, {req_id: top-2 logit margins} (with
+    `record_margins`, through a sampler that also takes the argmax), stats from the step log)."""
+    import torch
+
+    from minillm.engine.core import AddRequest, EngineCore
+
+    margins, pending = {}, {}
+
+    def greedy_with_margins(reqs, logits):
+        top2 = logits.float().topk(2, dim=-1).values
+        for r, m in zip(reqs, (top2[:, 0] - top2[:, 1]).tolist()):
+            pending[r.req_id] = m
+        return logits.argmax(dim=-1).tolist()
+
+    model.set_backend(backend)
+    core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=len(prompts), num_kv_blocks=blocks,
+                      enable_prefix_caching=False, metadata_builder=builder, chunked_prefill=chunked_prefill,
+                      max_num_batched_tokens=max_num_batched_tokens,
+                      kv_cache_dtype=torch.float8_e4m3fn if kv_fp8 else None, decode_graphs=decode_graphs,
+                      sampler=greedy_with_margins if record_margins else None)
+    for i, p in enumerate(prompts):
+        core.add_request(AddRequest(f"r{i}", p, decode_steps, ignore_eos=True))
+    out = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while core.has_work():
+        for o in core.step().outputs:
+            out.setdefault(o.req_id, []).extend(o.new_token_ids)
+            if record_margins:
+                margins.setdefault(o.req_id, []).append(pending[o.req_id])
+    wall = time.perf_counter() - t0
+    dec = [r for r in core.step_log if r.decode_tokens]
+    pre = [r for r in core.step_log if r.prefill_tokens]
+    generated = sum(len(v) for v in out.values())
+    stats = {"decode_tokens_per_s": sum(r.decode_tokens for r in dec) / (sum(r.duration_ns for r in dec) * 1e-9),
+             "output_tokens_per_s": generated / (sum(r.duration_ns for r in core.step_log) * 1e-9),
+             "mixed_steps": sum(1 for r in core.step_log if r.decode_tokens and r.prefill_tokens),
+             "decode_steps": len(dec), "prefill_steps": len(pre),
+             "prefill_tokens_per_s": sum(r.prefill_tokens for r in pre) / (sum(r.duration_ns for r in pre) * 1e-9),
+             "median_decode_step_ms": statistics.median(r.duration_ns for r in dec) * 1e-6,
+             "wall_s": wall, "preemptions": core.stats().num_preemptions}
+    del core
+    torch.cuda.empty_cache()
+    return out, margins, stats
+
+
 def bench_engine(args):
     """End-to-end engine on a random-init Llama-3.1-8B (bf16 weights ~ N(0, 0.02), seed 0): `--requests`
     prompts of 256-2048 random tokens, each decoded greedily for `--decode-steps` tokens, continuously
     batched (all requests admitted up to 8192 prompt tokens per prefill step), 16-token blocks, pool
     sized for 90% occupancy.  Reports decode tokens/s over the decode steps (StepRecord durations)."""
-    import torch
-
     from minillm.attention import get_backend
-    from minillm.engine.core import AddRequest, EngineCore
-    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
-    from minillm.model.llama import LlamaForCausalLM, random_init_
 
-    dev = torch.device("cuda:0")
-    cfg = LlamaConfig(**LLAMA_3_1_8B)
-    with torch.device("meta"):
-        model = LlamaForCausalLM(cfg)
-    model = model.to_empty(device=dev).to(torch.bfloat16)
-    random_init_(model, std=0.02, seed=0)
-    g = torch.Generator().manual_seed(0)
-    lens = torch.randint(256, 2049, (args.requests,), generator=g).tolist()
-    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
-    blocks = -(-sum(-(-(n + args.decode_steps) // 16) for n in lens) * 10 // 9)
+    model, prompts, blocks = engine_8b_model(args.requests, args.decode_steps)
 
-    def run(backend, builder):
-        model.set_backend(backend)
-        core = EngineCore(model, max_model_len=4096, step_log=True, max_batch_size=args.requests,
-                          num_kv_blocks=blocks, enable_prefix_caching=False, metadata_builder=builder,
+    def run(backend, builder, record_margins=False):
+        return engine_run(model, prompts, blocks, backend, builder, args.decode_steps,
                           chunked_prefill=args.chunked_prefill, max_num_batched_tokens=args.max_num_batched_tokens,
-                          kv_cache_dtype=torch.float8_e4m3fn if args.kv_dtype == "fp8" else None,
-                          decode_graphs=args.decode_graphs and backend is hip_backend)
-        for i, p in enumerate(prompts):
-            core.add_request(AddRequest(f"r{i}", p, args.decode_steps, ignore_eos=True))
-        out, margins, last = {}, {}, {}
-        hook = model.register_forward_hook(lambda mod, a, o: last.__setitem__("l", o))
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        while core.has_work():
-            step = core.step()
-            top2 = last["l"][:, -1].float().topk(2, dim=-1).values
-            for o, m in zip(step.outputs, (top2[:, 0] - top2[:, 1]).tolist()):
-                out.setdefault(o.req_id, []).extend(o.new_token_ids)
-                margins.setdefault(o.req_id, []).append(m)
-        wall = time.perf_counter() - t0
-        hook.remove()
-        dec = [r for r in core.step_log if r.decode_tokens]
-        pre = [r for r in core.step_log if r.prefill_tokens]
-        generated = sum(len(v) for v in out.values())
-        stats = {"decode_tokens_per_s": sum(r.decode_tokens for r in dec) / (sum(r.duration_ns for r in dec) * 1e-9),
-                 "output_tokens_per_s": generated / (sum(r.duration_ns for r in core.step_log) * 1e-9),
-                 "mixed_steps": sum(1 for r in core.step_log if r.decode_tokens and r.prefill_tokens),
-                 "decode_steps": len(dec), "prefill_steps": len(pre),
-                 "prefill_tokens_per_s": sum(r.prefill_tokens for r in pre) / (sum(r.duration_ns for r in pre) * 1e-9),
-                 "median_decode_step_ms": statistics.median(r.duration_ns for r in dec) * 1e-6,
-                 "wall_s": wall, "preemptions": core.stats().num_preemptions}
-        del core
-        torch.cuda.empty_cache()
-        return out, margins, stats
+                          kv_fp8=args.kv_dtype == "fp8", decode_graphs=args.decode_graphs and backend is hip_backend,
+                          record_margins=record_margins)
 
     hip_backend = get_backend("hip")
     hip_backend.fuse_rotary = not args.unfused_rotary
@@ -248,7 +278,7 @@ def bench_engine(args):
     if args.compare_oracle:
         from oracle_engine import OracleBackend, oracle_metadata
 
-        exp, margins, st_ref = run(OracleBackend(), oracle_metadata)
+        exp, margins, st_ref = run(OracleBackend(), oracle_metadata, record_margins=True)
         same = sum(got[r] == exp[r] for r in exp)
         first_div = []
         for r in exp:
@@ -436,6 +466,28 @@ def kernel_rates(wl, r, kv_elem: int) -> dict:
     return out
 
 
+def engine_subline() -> dict:
+    """The end-to-end engine (random-init Llama-3.1-8B, 128 requests x 256 greedy tokens, eager steps) as a
+    sub-line of the default run; an error there is reported in the line instead of ending the run."""
+    import torch
+
+    from minillm.attention import get_backend
+
+    model = None
+    try:
+        model, prompts, blocks = engine_8b_model(128, 256)
+        _, _, st = engine_run(model, prompts, blocks, get_backend("hip"), None, 256)
+        out = {k: round(v, 3) if isinstance(v, float) else v for k, v in st.items()}
+        out["workload"] = (f"engine_8b: 128 requests, prompts U[256, 2048], 256 greedy tokens each, pool {blocks} "
+                           f"blocks (90% occupancy), prefill-first, RoPE fused into the KV append")
+        return out
+    except Exception as e:  # noqa: BLE001 - the headline line must still print
+        return {"error": f"{type(e).__name__}: {e}"}
+    finally:
+        del model
+        torch.cuda.empty_cache()
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -535,6 +587,7 @@ def main():
                                 "tokens_per_s_32_layers": round(swl.num_tokens / (LAYERS * t), 2)}
             configs[f"{name}_fp8" if sub_fp8 else name] = entry
             torch.cuda.empty_cache()
+        configs["engine_8b"] = engine_subline()
         line["configs"] = configs
     if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool, every row
         line["cpu_baseline"] = cpu_baseline(wl, args)
