@@ -271,3 +271,88 @@ def test_fp8_pool_engine_on_cpu():
     assert root_hash({**keys, "salt": ""}) != root_hash({**plain, "salt": ""})
     with pytest.raises(ValueError, match="fp8 pools only"):
         PagedKVCache(cfg, 4, "cpu", torch.bfloat16, k_scale=2.0)
+
+
+class _ListModel:
+    """The block manager's rules written out with plain lists: blank blocks in release order (initially
+    0 .. n-1), named idle blocks in least-recently-released order, holder counts per block."""
+
+    def __init__(self, n):
+        self.blank, self.named_idle, self.holders, self.named = list(range(n)), [], [0] * n, set()
+
+    def allocate(self, k):
+        out = []
+        for _ in range(k):
+            if self.blank:
+                b = self.blank.pop(0)
+            else:
+                b = self.named_idle.pop(0)
+                self.named.discard(b)
+            self.holders[b] = 1
+            out.append(b)
+        return out
+
+    def acquire(self, blocks):
+        for b in blocks:
+            if self.holders[b] == 0:
+                self.named_idle.remove(b)
+            self.holders[b] += 1
+
+    def free(self, table):
+        for b in reversed(table):
+            self.holders[b] -= 1
+            if self.holders[b] == 0:
+                (self.named_idle if b in self.named else self.blank).append(b)
+
+    def clear(self):
+        for b in self.named_idle:
+            self.named.discard(b)
+            self.blank.append(b)
+        self.named_idle = []
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_manager_random_churn_matches_the_rules(seed):
+    import random
+
+    rng = random.Random(seed)
+    n = rng.choice([8, 24, 64])
+    pc = PrefixCache()
+    bm, model = BlockManager(n, 16, pc), _ListModel(n)
+    tables, ticket = [], 0
+    for _ in range(600):
+        op = rng.random()
+        if op < 0.35:  # a new table
+            k = rng.randint(1, 4)
+            if k <= bm.num_free:
+                got = bm.allocate(k)
+                assert got == model.allocate(k)
+                tables.append(got)
+            else:
+                with pytest.raises(RuntimeError):
+                    bm.allocate(k)
+        elif op < 0.6 and tables:  # a table released, tail first
+            t = tables.pop(rng.randrange(len(tables)))
+            model.free(list(t))
+            bm.free(t)
+            assert t == []
+        elif op < 0.8 and tables:  # a held block filled and is named
+            b = rng.choice(rng.choice(tables))
+            ticket += 1
+            pc.insert(ticket.to_bytes(8, "little"), b)
+            model.named.add(b)
+        elif op < 0.95:  # a prefix hit: named blocks (held or idle) shared by a new table
+            cands = sorted(model.named)
+            if cands:
+                hit = rng.sample(cands, rng.randint(1, min(3, len(cands))))
+                bm.acquire(hit)
+                model.acquire(hit)
+                tables.append(list(hit))
+        else:
+            bm.clear_cache()
+            model.clear()
+        assert bm.num_free == len(model.blank) + len(model.named_idle)
+        assert bm.num_cached == len(model.named_idle)
+        assert all(bm.is_cached_unheld(b) == (b in model.named_idle) for b in range(n))
+        bm.check(tables)
+    assert {b for b in range(n) if pc.is_cached(b)} == model.named
