@@ -274,6 +274,9 @@ class StaticDecodeMetadata:
         cap = self._upd + 2 * num_rows * self.max_blocks
         self.pinned = torch.empty(cap, dtype=torch.int32, pin_memory=True)
         self.packed = torch.zeros(cap, dtype=torch.int32, device=dev)
+        # the last upload from `pinned`: the host waits for it before packing the next step into the same
+        # pinned memory (the copy runs when the stream reaches it, which may be after the host moved on)
+        self._uploaded = torch.cuda.Event()
         self.meta = AttentionMetadata._arenas(block_size, list(range(num_rows + 1)),
                                               [self.max_blocks * block_size] * num_rows, num_rows, self.max_blocks,
                                               num_rows * self.max_blocks, dev)
@@ -309,6 +312,7 @@ class StaticDecodeMetadata:
                 raise ValueError(f"a row of {len(s.block_ids)} blocks exceeds the graph's {self.max_blocks} blocks")
         rows, updates = self.tables.sync(keys, seqs)
         n, pad = len(seqs), b - len(seqs)
+        self._uploaded.synchronize()  # no-op before the first upload
         host = self.pinned.numpy()
         host[:n] = [s.num_cached for s in seqs]
         host[n:b] = 0
@@ -322,6 +326,7 @@ class StaticDecodeMetadata:
         host[self._upd:self._upd + u] = updates
         end = self._upd + u
         self.packed[:end].copy_(self.pinned[:end], non_blocking=True)
+        self._uploaded.record()
         self.tables.apply(self.packed, self._upd, u // 2)
         del pad
 

@@ -36,6 +36,7 @@ DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
 class _Captured:
     def __init__(self, static: StaticDecodeMetadata, ids: torch.Tensor, pinned_ids: torch.Tensor) -> None:
         self.static, self.ids, self.pinned_ids = static, ids, pinned_ids
+        self.ids_uploaded = torch.cuda.Event()  # the last copy out of pinned_ids
         self.graph: torch.cuda.CUDAGraph | None = None
         self.workspace: torch.Tensor | None = None  # the decode workspace the graph recorded
         self.logits: torch.Tensor | None = None  # [B, V] of the last replay
@@ -113,10 +114,14 @@ class DecodeGraphs:
         bs = self.block_size
         pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs)
         c.static.load(keys, seqs, pages_per_split(pages, self.num_kv_heads))  # the eager step's split size
+        # the previous step's copy out of the same pinned memory may still be queued behind its replay
+        # (a sampler need not wait for the GPU): let it run before the host rewrites the ids
+        c.ids_uploaded.synchronize()
         ids = c.pinned_ids.numpy()
         ids[:len(token_ids)] = token_ids
         ids[len(token_ids):] = 0
         c.ids.copy_(c.pinned_ids.view(1, -1), non_blocking=True)
+        c.ids_uploaded.record()
 
     def _body(self, c: _Captured):
         """The captured work: metadata build, then the forward (whose first layer builds the plan)."""

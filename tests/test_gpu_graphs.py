@@ -61,6 +61,48 @@ def test_graph_engine_matches_eager_engine(hip, kv):
     assert core.graphs.replays > 10 and len(core.graphs._captured) >= 2  # batch shrinks as requests finish
 
 
+def test_host_running_ahead_of_the_gpu_changes_nothing(hip):
+    # a sampler that returns its tokens without reading the GPU lets the host stage the next replay while
+    # the GPU still works on earlier steps (held back here by a bounded spin kernel per step): the staged
+    # inputs of a later step must not reach a step still queued
+    from minillm.attention import get_backend
+    from minillm.engine.core import AddRequest, EngineCore
+
+    model = tiny_model(seed=61)
+    model.set_backend(get_backend("hip"))
+    ps = prompts(6, 1, 120, seed=62)
+
+    def run(sampler):
+        core = EngineCore(model, max_batch_size=8, num_kv_blocks=200, max_model_len=2048, decode_graphs=True,
+                          sampler=sampler)
+        for i, p in enumerate(ps):
+            core.add_request(AddRequest(f"r{i}", p, 24, ignore_eos=True))
+        out = {}
+        while core.has_work():
+            for o in core.step().outputs:
+                out.setdefault(o.req_id, []).extend(o.new_token_ids)
+        return out, core
+
+    def keeper(store, tokens=None):
+        def sample(reqs, logits):
+            for r, row in zip(reqs, logits):
+                store[(r.req_id, len(r.output))] = row.clone()
+            if tokens is None:
+                return logits.argmax(dim=-1).tolist()  # reads the GPU: host and GPU in step
+            torch.cuda._sleep(20_000_000)
+            return [tokens[r.req_id][len(r.output)] for r in reqs]  # never waits for the GPU
+        return sample
+
+    synced, ahead = {}, {}
+    tokens, core = run(keeper(synced))
+    forced, core2 = run(keeper(ahead, tokens))
+    torch.cuda.synchronize()
+    assert core.graphs.replays > 10 and core2.graphs.replays == core.graphs.replays
+    assert forced == tokens and synced.keys() == ahead.keys()
+    for key, row in synced.items():
+        assert torch.equal(row.view(torch.int16), ahead[key].view(torch.int16)), key
+
+
 def test_graph_rejects_what_it_cannot_hold(hip):
     from minillm.attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata
 
