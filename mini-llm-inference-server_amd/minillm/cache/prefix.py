@@ -80,5 +80,8 @@ class PrefixCache:
             self._name_by_block[block] = None
 
     def clear(self) -> None:
+        """Drops every name.  Only for a cache no block manager is using: a manager keeps counts of the idle
+        blocks it parked as named (an engine clears through BlockManager.clear_cache, which drops the names
+        of idle blocks only)."""
         self._block_by_name.clear()
         self._name_by_block.clear()
