@@ -27,6 +27,7 @@ workloads on the GPU with their own kernels' rates and the same CPU baseline:
     python bench.py --workload engine_8b [--compare-oracle]   # end-to-end engine, random-init Llama-3.1-8B
     python bench.py --workload copy_1gib                      # counter calibration: a 1 GiB device copy
     python bench.py --workload gemm_8192                      # attainable bf16 MFMA rate of a library GEMM
+    python bench.py --workload decode_uniform_384x89          # decode_256's bytes in equal rows (no tail)
     python bench.py --kv-dtype fp8                            # the same step on an fp8 (e4m3fn) pool
     python bench.py --workload prefix_64 --no-configs --no-cpu-baseline   # one workload alone (profiling)
 
@@ -508,7 +509,7 @@ def main():
     if args.workload == "gemm_8192":
         return gemm_calibration()
     dev = torch.device("cuda:0")
-    wl = workloads.WORKLOADS[args.workload]()
+    wl = workloads.by_name(args.workload)
     fp8 = args.kv_dtype == "fp8"
     kv_elem = 1 if fp8 else 2
     backend = HipBackend()

@@ -10,6 +10,7 @@ the CPU) sees identical bytes; page assignment is a seeded `randperm` of the poo
                   0-1024 cached) + 120 decode rows (context uniform in [256, 8192]), seeded row order.
 - `prefix_64`     64 rows sharing one 2048-token prefix (128 pages present in every block table) with
                   a private suffix of 64-512 new tokens each.
+- `decode_uniform_<rows>x<pages>`  rows of exactly `pages` pages each (a load-balance bound for decode).
 
 Work per layer (the denominators of the reported rates):
   bytes  B = sum_s L_s*Hkv*Dh*2*2 (context K+V, appended token included) + N*H*Dh*2*2 (q in, o out)
@@ -153,4 +154,28 @@ def prefix_64(seed: int = 0, dtype=torch.bfloat16) -> Workload:
     return _finish("prefix_64", g, steps, tables, pool, notes={"shared_pages": prefix_pages}, dtype=dtype)
 
 
+def decode_uniform(rows: int, pages: int, seed: int = 0, dtype=torch.bfloat16) -> Workload:
+    """`rows` decode rows of exactly `pages` full pages each (the appended token fills the last one), pool
+    and page assignment as decode_256's.  When the split size comes out at `pages` (or a divisor), every
+    row and KV head is one equal item: a launch with no tail.  At 384 x 89 it holds decode_256's bytes
+    within 0.3%, the load-balance bound of that workload."""
+    g = torch.Generator().manual_seed(seed)
+    steps = [(pages * BS - 1, 1)] * rows
+    lens = [pages * BS] * rows
+    pool = 2 * rows * pages
+    return _finish(f"decode_uniform_{rows}x{pages}", g, steps, _assign(g, lens, pool), pool,
+                   notes={"rows": rows, "pages": pages}, dtype=dtype)
+
+
 WORKLOADS = {"decode_4": decode_4, "decode_256": decode_256, "mixed_128": mixed_128, "prefix_64": prefix_64}
+
+
+def by_name(name: str) -> Workload:
+    """A workload of WORKLOADS, or `decode_uniform_<rows>x<pages>`."""
+    if name in WORKLOADS:
+        return WORKLOADS[name]()
+    if name.startswith("decode_uniform_"):
+        rows, _, pages = name.removeprefix("decode_uniform_").partition("x")
+        if rows.isdigit() and pages.isdigit() and int(rows) > 0 and int(pages) > 0:
+            return decode_uniform(int(rows), int(pages))
+    raise ValueError(f"unknown workload {name!r}: one of {sorted(WORKLOADS)} or decode_uniform_<rows>x<pages>")

@@ -115,6 +115,23 @@ def test_workloads_are_deterministic_and_sized():
     assert len(set(used)) == len(used) and max(used) < a.num_blocks
 
 
+def test_uniform_decode_workload_has_equal_full_rows():
+    # decode_uniform_<rows>x<pages>: every row exactly `pages` full pages after the append, one new token,
+    # distinct pages; at 384 x 89 the split heuristic picks 89, so every row is one equal item
+    from minillm import workloads
+    from minillm.attention import hip_backend
+
+    w = workloads.by_name("decode_uniform_6x5")
+    assert w.name == "decode_uniform_6x5" and len(w.seqs) == 6
+    assert all(n == 1 and c + n == 5 * 16 and len(t) == 5 for c, n, t in w.seqs)
+    used = [b for _, _, t in w.seqs for b in t]
+    assert len(set(used)) == len(used) and max(used) < w.num_blocks == 60
+    assert hip_backend.pages_per_split(384 * 89, 8) == 89
+    for bad in ("decode_uniform_0x5", "decode_uniform_3", "decode_512"):
+        with pytest.raises(ValueError):
+            workloads.by_name(bad)
+
+
 def test_packed_step_upload_layout():
     # num_cached[S] | num_new[S] | table_indptr[S+1] | table_ids: the one upload the GPU build reads
     import numpy as np
