@@ -500,7 +500,7 @@ def main():
     import torch
 
     from minillm import workloads
-    from minillm.attention.hip_backend import HipBackend
+    from minillm.attention.hip_backend import HipBackend, decode_kernel_name
 
     if args.workload == "engine_8b":
         return bench_engine(args)
@@ -526,12 +526,13 @@ def main():
         dec_bytes = wl.decode_kernel_bytes(kv_elem)
         achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
         traffic = None
-        tfile = ROOT / "profiles" / f"decode_kernel_{wl.name}{'_fp8' if fp8 else ''}_traffic.json"
+        kname = decode_kernel_name(fp8, wl.h, wl.hkv)
+        tfile = ROOT / "profiles" / f"{kname}_{wl.name}{'_fp8' if fp8 else ''}_traffic.json"
         if tfile.exists():
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                    "kernel": "decode_kernel", "algorithmic_bytes": dec_bytes, "mean_us": round(dec_ms * 1e3, 2)}
+                    "kernel": kname, "algorithmic_bytes": dec_bytes, "mean_us": round(dec_ms * 1e3, 2)}
     else:
         flops = wl.prefill_flops()
         achieved = flops / (pf_ms * 1e-3) / 1e12

@@ -15,12 +15,15 @@
 // Rows with one chunk write the normalised output; longer rows write fp32 (m, l, acc) partials that a
 // second kernel merges with a log-sum-exp.
 //
-// fp8 (e4m3fn) pools: a tile is half the bytes.  Each lane loads K row (l % 16) as two 16-byte pieces,
-// dims 64 h + 16 (l / 16) .. +15 for h = 0, 1, so S^T's k-dimension runs through the dims in that
-// order (the Q^T operand is loaded in the same order; a dot product does not depend on it), and V rows
-// 4 (l / 16) .. +3 at dims 8 (l % 16) .. +7 as four 8-byte pieces.  The tile is widened to bf16/fp16 in
-// registers (v_cvt_scalef32_pk_*_fp8 with scale 1: exact) right before it is consumed, so the MFMA
-// stream is the 16-bit one; k_scale is folded into the softmax scale and v_scale into the output.
+// fp8 (e4m3fn) pools with an even number of KV heads and at most 8 query heads per KV head run
+// decode_pair_kernel (below): two KV heads per wavefront, loaded with the 16-bit kernel's shapes.  Other
+// fp8 pools run this kernel with one head per wavefront, where a tile is half the bytes.  Each lane
+// loads K row (l % 16) as two 16-byte pieces, dims 64 h + 16 (l / 16) .. +15 for h = 0, 1, so S^T's
+// k-dimension runs through the dims in that order (the Q^T operand is loaded in the same order; a dot
+// product does not depend on it), and V rows 4 (l / 16) .. +3 at dims 8 (l % 16) .. +7 as four 8-byte
+// pieces.  The tile is widened to bf16/fp16 in registers (v_cvt_scalef32_pk_*_fp8 with scale 1: exact)
+// right before it is consumed, so the MFMA stream is the 16-bit one; k_scale is folded into the softmax
+// scale and v_scale into the output.
 #include <math.h>
 
 #include <mutex>
@@ -315,6 +318,204 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   }
 }
 
+// fp8 pools, two adjacent KV heads per wavefront (heads 2j and 2j + 1).  Their 128-byte rows of one
+// token are one 256-byte row of the pool, so the pair is loaded exactly as the 16-bit kernel loads one
+// head: K row c as four 16-byte pieces (bytes 64 p + 16 g .. +15, p = 0..3; pieces 0-1 are head A's,
+// 2-3 head B's) and V rows 4 g + i as one 16-byte piece each (bytes 16 c .. +15: lanes c < 8 hold head
+// A's dims 16 c .., lanes c >= 8 head B's dims 16 (c - 8) ..).  A 16-token tile is 8 KB, as in the
+// 16-bit kernel.
+//   S^T[16 tok x 16] = [K_A | K_B] . [Q_A^T ; Q_B^T]   8 x v_mfma_f32_16x16x32 over k = 256
+// Columns 0 .. G-1 are head A's query heads, G .. 2G-1 head B's; a column's Q^T operand is zero on the
+// other head's k-steps, so one product gives both heads' scores and the softmax runs once for the pair.
+//   O^T[16 x 16]_m += V^T_m[16 x 16 tok] . P^T[16 tok x 16], m = 0..15   16 x v_mfma_f32_16x16x16
+// Row r of product m is element m of V lane r's 16 dims: head A dim 16 r + m for r < 8, head B dim
+// 16 (r - 8) + m for r >= 8.  Only head A's columns of rows 0-7 and head B's columns of rows 8-15 are
+// kept, so lane (c, g) ends holding dims 64 (g & 1) + 16 i + m of query head 2j G + c when
+// c < G and g < 2 or G <= c < 2G and g >= 2.  Same MFMA count per head as the one-head kernel, half the
+// softmax and load instructions per head.
+struct PairTile {
+  u32x4 k[4];
+  u32x4 v[4];
+};
+
+template <bool NT>
+__device__ __forceinline__ void load_pair(const DecodeArgs& a, const char* kbase, const char* vbase, int64_t tok_stride,
+                                          int64_t blk_stride, int page_lo, int page_hi, LoadCursor at, int c, int g,
+                                          PairTile& r) {
+  int blk = __builtin_amdgcn_readlane(at.page < 64 ? page_lo : page_hi, at.page & 63);
+  if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
+  const int64_t off = (int64_t)blk * blk_stride + (int64_t)(at.sub * 16) * tok_stride;
+  const char* kp = kbase + off + c * tok_stride;
+  const char* vp = vbase + off + (4 * g) * tok_stride;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r.k[p] = ldkv<NT>(kp + 64 * p + 16 * g);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = ldkv<NT>(vp + (int64_t)i * tok_stride + 16 * c);
+}
+
+// One 16-token tile of a head pair.  qa / qb: the Q^T operands of head A's and head B's k-steps (zero in
+// the other head's columns).
+template <typename T>
+__device__ __forceinline__ void consume_pair(PairTile& r, const u32x4 (&qa)[4], const u32x4 (&qb)[4], float scale_log2,
+                                             int tpos0, int len, int g, float& m_run, float& l_run, f32x4 (&o)[16]) {
+  f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const u32x4 (&qh)[4] = p < 2 ? qa : qb;
+    sc = Mfma<T>::m16x16x32(fp8x8_to<T>(r.k[p][0], r.k[p][1]), qh[2 * (p & 1)], sc);
+    sc = Mfma<T>::m16x16x32(fp8x8_to<T>(r.k[p][2], r.k[p][3]), qh[2 * (p & 1) + 1], sc);
+  }
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
+  if (tpos0 + 16 > len) {  // the row's last, partly filled tile: mask the keys past its end, zero their V
+    const int tpos = tpos0 + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tpos + i >= len) {
+        s[i] = -INFINITY;
+        r.v[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+  const float mx = maximum_xor32(maximum_xor16(maximum(maximum(s[0], s[1]), maximum(s[2], s[3]))));
+  if (__any(mx > m_run + 8.f)) {  // lazy rescale, as in the one-head kernel
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) o[m] *= alpha;
+    m_run = m_new;
+  }
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_run);
+  l_run += sum_xor32(sum_xor16((p[0] + p[1]) + (p[2] + p[3])));
+  const u32x2 pfrag = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {  // elements 4 b .. 4 b + 3 of the four V rows, widened just in time
+    u32x2 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = fp8x4_to<T>(r.v[i][b]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int dw = e >> 1, hf = e & 1;
+      const u32x2 vfrag = u32x2{pick_halves(w[0][dw], hf, w[1][dw], hf), pick_halves(w[2][dw], hf, w[3][dw], hf)};
+      o[4 * b + e] = Mfma<T>::m16x16x16(vfrag, pfrag, o[4 * b + e]);
+    }
+  }
+}
+
+template <typename T, int W, int PF, bool NT, int OCC>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_pair_kernel(
+    const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  // a workgroup of W wavefronts covers 2 W KV heads of one item; HG = ceil(Hkv / (2 W)) groups per item
+  const int hg = blockIdx.x % a.HG;
+  const int item = blockIdx.x / a.HG;
+  const int kvh0 = 2 * (hg * W + (threadIdx.x >> 6));
+  if (kvh0 >= a.Hkv) return;  // wave-uniform
+  const int4 w = a.work[item];
+  const int seq = w.x, split = w.y, nsplit = w.z, slot = w.w;
+  if (seq < 0) return;  // unfilled plan slot
+  const int pg0 = a.kv_indptr[seq];
+  const int npg = a.kv_indptr[seq + 1] - pg0;
+  const int len = a.seq_lens[seq];
+  const int pb = pg0 + (int)(((int64_t)split * npg) / nsplit);
+  const int pe = pg0 + (int)(((int64_t)(split + 1) * npg) / nsplit);
+  const int tok0 = (pb - pg0) * a.bs;
+  const int tok1 = min(len, (pe - pg0) * a.bs);
+  const int ntiles = (tok1 - tok0 + 15) >> 4;
+  const int tpp = a.bs >> 4;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int qtok = a.qo_indptr[seq];
+  const int page_lo = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
+  const int page_hi = lane + 64 < (pe - pb) ? a.kv_indices[pb + 64 + lane] : 0;
+
+  // column c: query head 2j G + c (head A's for c < G, head B's for G <= c < 2G); k-step t of a head
+  // covers its dims 64 (t >> 1) + 16 g + 8 (t & 1) .. +7
+  const bool qvalid = c < 2 * a.G;
+  const bool in_b = c >= a.G;
+  u32x4 qa[4], qb[4];
+  {
+    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qtok * a.q_st +
+                                                   (int64_t)(kvh0 * a.G + (qvalid ? c : 0)) * a.q_sh);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 v = ld16(qp + 2 * (64 * (t >> 1) + 16 * g + 8 * (t & 1)));
+      const u32x4 z = u32x4{0, 0, 0, 0};
+      qa[t] = qvalid && !in_b ? v : z;
+      qb[t] = qvalid && in_b ? v : z;
+    }
+  }
+
+  const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;  // one byte per element
+  const int64_t blk_stride = (int64_t)a.bs * tok_stride;
+  const char* kbase = a.kc + kvh0 * kHeadDim;
+  const char* vbase = a.vc + kvh0 * kHeadDim;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int R = PF + 1;
+  PairTile ring[R];
+  LoadCursor next;
+#pragma unroll
+  for (int r = 0; r < PF; ++r)
+    if (r < ntiles) {
+      load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[r]);
+      next.advance(tpp);
+    }
+  for (int t0 = 0; t0 < ntiles; t0 += R) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int t = t0 + r;
+      if (t < ntiles) {
+        if (t + PF < ntiles) {
+          load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[(r + PF) % R]);
+          next.advance(tpp);
+        }
+        consume_pair<T>(ring[r], qa, qb, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+      }
+    }
+  }
+
+  // lanes that hold kept rows: head A's columns in lane groups 0-1, head B's in 2-3
+  if (!qvalid || in_b != (g >= 2)) return;
+  const int head = kvh0 * a.G + c;
+  const int d0 = 64 * (g & 1);  // o[m][i] is dim d0 + 16 i + m
+  if (nsplit == 1) {
+    const float inv = a.v_scale / l_run;
+    char* op = reinterpret_cast<char*>(a.out + (int64_t)qtok * a.o_st + (int64_t)head * a.o_sh + d0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int m = 8 * h;
+        const u32x4 pk = u32x4{pack2<T>(o[m][i] * inv, o[m + 1][i] * inv), pack2<T>(o[m + 2][i] * inv, o[m + 3][i] * inv),
+                               pack2<T>(o[m + 4][i] * inv, o[m + 5][i] * inv), pack2<T>(o[m + 6][i] * inv, o[m + 7][i] * inv)};
+        st16(op + 2 * (16 * i + m), pk);
+      }
+    }
+  } else {
+    const int64_t row = (int64_t)slot * a.H + head;
+    float* po = a.part_o + row * kHeadDim + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int m = 4 * q4;
+        *reinterpret_cast<f32x4*>(po + 16 * i + m) =
+            f32x4{o[m][i] * a.v_scale, o[m + 1][i] * a.v_scale, o[m + 2][i] * a.v_scale, o[m + 3][i] * a.v_scale};
+      }
+    }
+    if ((g & 1) == 0) a.part_ml[row] = make_float2(m_run, l_run);
+  }
+}
+
 // Log-sum-exp merge of a row's split partials: one workgroup per (row, head), one thread per dim.
 template <typename T>
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict__ merge, const float* __restrict__ part_o,
@@ -373,7 +574,7 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
 constexpr int kPrefetch = MLLM_DECODE_PREFETCH;
 constexpr bool kNonTemporal = true;
 constexpr int kOccupancy = MLLM_DECODE_OCC;
-// fp8 tiles hold half the bytes in half the registers, and widening them adds VALU work per byte: four
+// One-head fp8 kernel: fp8 tiles hold half the bytes in half the registers, and widening them adds VALU work per byte: four
 // tiles of lookahead at 2 wavefronts per SIMD (171 VGPRs, no spill) measured 198.3-198.7 us on
 // decode_256 (5.62-5.63 TB/s), against 203-204 us for 3 tiles at 3 per SIMD, 205 us for 1 at 4 and
 // 213 us for 2 at 3 (same box, alternating); 5 and 6 tiles at 2 per SIMD match 4, 8 is 1% slower.
@@ -386,8 +587,39 @@ constexpr int kPrefetchFp8 = MLLM_DECODE_FP8_PREFETCH;
 #endif
 constexpr int kOccupancyFp8 = MLLM_DECODE_FP8_OCC;
 
+// The pair kernel (fp8, two KV heads per wavefront): W wavefronts per workgroup, PF tiles of lookahead at
+// OCC wavefronts per SIMD.  On decode_256: 4 / 2 / 2 (221 VGPRs) 192-195 us; 4 / 1 / 2 the same; 2 per
+// workgroup 199-204 us and 1 per workgroup 212-214 us (a workgroup on all 8 KV heads reads whole pages);
+// the one-head kernel 198 us on the same box.
+#ifndef MLLM_DECODE_PAIR_WAVES
+#define MLLM_DECODE_PAIR_WAVES 4
+#endif
+constexpr int kWavesPair = MLLM_DECODE_PAIR_WAVES;
+#ifndef MLLM_DECODE_PAIR_PREFETCH
+#define MLLM_DECODE_PAIR_PREFETCH 2
+#endif
+#ifndef MLLM_DECODE_PAIR_OCC
+#define MLLM_DECODE_PAIR_OCC 2
+#endif
+constexpr int kPrefetchPair = MLLM_DECODE_PAIR_PREFETCH;
+constexpr int kOccupancyPair = MLLM_DECODE_PAIR_OCC;
+
+// fp8 pools run the pair kernel when the KV heads pair up and a pair's query heads fit 16 columns.
+__host__ __device__ constexpr bool pair_heads(int num_kv_heads, int group) {
+  return num_kv_heads % 2 == 0 && 2 * group <= 16;
+}
+
 template <typename T, bool F8>
 int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
+  if constexpr (F8) {
+    if (pair_heads(a.Hkv, a.G)) {
+      DecodeArgs b = a;
+      b.HG = (a.Hkv + 2 * kWavesPair - 1) / (2 * kWavesPair);
+      decode_pair_kernel<T, kWavesPair, kPrefetchPair, kNonTemporal, kOccupancyPair>
+          <<<(unsigned)n_work * (unsigned)b.HG, 64 * kWavesPair, 0, st>>>(b);
+      return check_launch("mllm_paged_decode_fp8");
+    }
+  }
   const unsigned grid = (unsigned)n_work * (unsigned)a.HG;
   decode_kernel<T, F8, F8 ? kPrefetchFp8 : kPrefetch, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy>
       <<<grid, 64 * kWaves, 0, st>>>(a);

@@ -64,6 +64,13 @@ def _ptr(t: torch.Tensor | None) -> int:
 FP8 = torch.float8_e4m3fn
 
 
+def decode_kernel_name(kv_fp8: bool, num_heads: int, num_kv_heads: int) -> str:
+    """The decode kernel mllm_paged_decode(_fp8) launches: fp8 pools pair adjacent KV heads in one wavefront
+    when the KV heads are even and a pair's query heads fit 16 MFMA columns."""
+    pair = kv_fp8 and num_kv_heads % 2 == 0 and 2 * (num_heads // num_kv_heads) <= 16
+    return "decode_pair_kernel" if pair else "decode_kernel"
+
+
 def is_fp8(pool: torch.Tensor) -> bool:
     return pool.dtype == FP8
 

@@ -132,6 +132,18 @@ def test_group_sizes_and_blocks(hip, h, hkv, bs):
     _check(*fp8_step(wl, 0.02, 0.02))
 
 
+@pytest.mark.parametrize("h,hkv", [(12, 3), (12, 6), (10, 2), (20, 4), (40, 10), (14, 2)],
+                         ids=["odd-hkv", "hkv6", "g5", "g5-hkv4", "hkv10", "g7"])
+def test_decode_head_pairing(hip, h, hkv):
+    # fp8 decode pairs adjacent KV heads in one wavefront when the KV heads are even and a pair's query
+    # heads fit the 16 MFMA columns, else runs one head per wavefront: odd KV heads, workgroups whose
+    # last wavefronts have no pair (6 and 10 KV heads), 5 and 7 query heads per KV head (unused columns);
+    # decode rows only, short and split
+    steps = [(0, 1), (90, 1), (300, 1), (17, 1), (1000, 1), (129, 1), (15, 1), (16, 1)]
+    wl = _kernel_case(h=h, hkv=hkv, steps=steps, num_blocks=200, seed=hkv)
+    _check(*fp8_step(wl, 0.03, 0.04))
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_random_mixed_steps(hip, seed):
     # seeded random steps with every row kind at the Llama GQA shape, fp8 pools with random scales
