@@ -22,7 +22,7 @@ def gpu_available() -> bool:
 
 @pytest.fixture(scope="session")
 def hip():
-    """The loaded HIP library.  GPU tests fail loudly (not skip) when it is missing on a GPU box."""
+    """The loaded HIP library.  GPU tests fail loudly (not skip) when it is missing on a machine with a GPU."""
     import torch
 
     if not torch.cuda.is_available():
