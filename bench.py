@@ -20,6 +20,8 @@ workloads on the GPU with their own kernels' rates and the same CPU baseline:
               its own launch, decode launch GB/s, and the step with both launches overlapped;
   prefix_64   64 rows over a shared 2,048-token prefix: prefill launch TFLOP/s and fraction;
   decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction;
+  gemm_8192   torch.mm (hipBLASLt) on 8192^3 bf16 operands, random and zero: the MFMA rate this GPU
+              sustains for a library GEMM; the prefill sub-lines also report their rate against it;
   engine_8b   the end-to-end engine on a random-init Llama-3.1-8B, 128 requests x 256 greedy tokens:
               decode tokens/s over its decode steps.
 
@@ -311,7 +313,7 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
 
 
-def gemm_calibration():
+def gemm_rates() -> dict:
     """The attainable bf16 MFMA rate of a library GEMM on this GPU: torch.mm (hipBLASLt) on 8192^3 bf16
     operands, random N(0, 1) and all-zero (the clock the MFMA stream sustains depends on the data it
     switches), each the mean of 20 launches after 5 warm-up ones."""
@@ -339,7 +341,13 @@ def gemm_calibration():
         ms = e0.elapsed_time(e1) / 20
         out[f"{name}_us"] = round(ms * 1e3, 1)
         out[f"{name}_tflops"] = round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)
-    print(json.dumps(out), flush=True)
+        del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
+def gemm_calibration():
+    print(json.dumps(gemm_rates()), flush=True)
 
 
 def shared_step_costs(wl, backend, dev, reps: int = 10):
@@ -589,6 +597,14 @@ def main():
                                 "tokens_per_s_32_layers": round(swl.num_tokens / (LAYERS * t), 2)}
             configs[f"{name}_fp8" if sub_fp8 else name] = entry
             torch.cuda.empty_cache()
+        # the MFMA rate a library GEMM reaches on this GPU in the same run: the prefill launches' rates
+        # against it as well as against the nominal peak
+        gemm = gemm_rates()
+        configs["gemm_8192"] = gemm
+        for name in ("mixed_128", "prefix_64"):
+            gpu = configs.get(name, {}).get("gpu", {})
+            if gpu.get("prefill_tflops"):
+                gpu["prefill_frac_of_gemm_random"] = round(gpu["prefill_tflops"] / gemm["random_tflops"], 4)
         configs["engine_8b"] = engine_subline()
         line["configs"] = configs
     if not args.no_cpu_baseline:  # the reference's own format: the oracle on the bf16 pool, every row
