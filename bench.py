@@ -508,7 +508,7 @@ def main():
     import torch
 
     from minillm import workloads
-    from minillm.attention.hip_backend import HipBackend, decode_kernel_name
+    from minillm.attention.hip_backend import HipBackend, decode_kernel_name, prefill_kernel_name
 
     if args.workload == "engine_8b":
         return bench_engine(args)
@@ -545,7 +545,7 @@ def main():
         flops = wl.prefill_flops()
         achieved = flops / (pf_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "prefill_kernel",
+                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": prefill_kernel_name(fp8),
                     "algorithmic_flops": flops, "mean_us": round(pf_ms * 1e3, 2)}
 
     line = {

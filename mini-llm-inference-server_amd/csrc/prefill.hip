@@ -21,7 +21,8 @@
 //
 // The two halves of the workgroup run phase-shifted (see prefill_kernel): one half's matrix phase
 // coincides with the other half's softmax, so every SIMD has an MFMA stream and a vector stream at
-// once.  Tiles entirely above a wavefront's causal diagonal are skipped.  Keys past the workgroup's
+// once.  With 16-bit pools a phase covers two tiles (prefill128_kernel: 128 keys per phase, one
+// softmax over both score tiles); with fp8 pools one tile (prefill_kernel).  Tiles entirely above a wavefront's causal diagonal are skipped.  Keys past the workgroup's
 // last visible key are loaded as copies of that key's row (their scores are masked, so P is exactly
 // 0 and pool slots past a row's length are never read).  The grid is 1-D with the KV head fastest,
 // so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and
@@ -49,6 +50,13 @@ constexpr int kVBase = kRingK * kTileBytes;  // byte offset of the V ring
 constexpr int kIdBase = (kRingK + kRingV) * kTileBytes;  // per wavefront two 64-entry windows of block ids
 constexpr int kLdsBytes = kIdBase + 8 * 2 * 64 * 4;
 constexpr int kQTileRows = 256;  // query rows (token x head of the group) per workgroup: 8 waves x 32
+// 16-bit pools run prefill128_kernel (128-key phases); 0 selects prefill_kernel (64-key phases), which
+// fp8 pools always run (their tiles pass through VGPRs, and two tiles of staging do not fit beside
+// the 128-key kernel's registers)
+#ifndef MLLM_PREFILL_128
+#define MLLM_PREFILL_128 1
+#endif
+constexpr bool kPrefill128 = MLLM_PREFILL_128;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -505,6 +513,247 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- 16-bit pools: 128-key phases
+// The same workgroup, tiles and operand layouts as prefill_kernel, but every phase covers two 64-key
+// tiles (a pair): the matrix phase of pair j runs PV of tiles 2j and 2j+1 and S of tiles 2j+2 and 2j+3
+// (64 MFMAs), and the vector phase runs one softmax over both score tiles (one max and one rescale
+// test per 128 keys).  Half the phases means half the barriers and per-phase bookkeeping per key:
+// prefix_64 674 us against 702-716 us for 64-key phases, mixed_128 76 against 78-80 us (same box).
+// Rings: K and V four tiles each (128 KB).  Even phase 2j loads V(2j+2), V(2j+3) into the slots of
+// V(2j-2), V(2j-1) and K(2j+4), K(2j+5) into those of K(2j), K(2j+1), all freed by the barrier that
+// ended phase 2j-1; the barrier ending phase 2j+1 waits for all of them (the next phase reads them).
+// A pair's second tile past the row (odd tile counts) or past a wavefront's last row is skipped in the
+// matrix phase and fully masked in the softmax, so its P is 0.
+constexpr int kRingK2 = 4, kRingV2 = 4;  // K and V tiles in LDS
+constexpr int kVBase2 = kRingK2 * kTileBytes;
+constexpr int kIdBase2 = (kRingK2 + kRingV2) * kTileBytes;
+constexpr int kLdsBytes2 = kIdBase2 + 8 * 2 * 64 * 4;
+
+// Online softmax of a pair of score tiles (keys kv0 .. kv0 + 127) -> the P^T operands of both PV
+// products, as softmax_tile does for one tile.
+template <typename T>
+__device__ __forceinline__ void softmax_two(STile& s0, STile& s1, u32x4 (&pf0)[2][2], u32x4 (&pf1)[2][2],
+                                            f32x16 (&oacc)[4], float& m_run, float& l_run, int kv0, int qp,
+                                            int wave_qp_lo, int h, float c) {
+  if (kv0 + 2 * kBN - 1 > wave_qp_lo) {  // some key of the pair lies past the wavefront's first row
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+        s0.s[b][r] = key > qp ? -INFINITY : s0.s[b][r];
+        s1.s[b][r] = key + kBN > qp ? -INFINITY : s1.s[b][r];
+      }
+  }
+  float m4[4] = {s0.s[0][0], s0.s[0][1], s0.s[0][2], s0.s[0][3]};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (b > 0 || r >= 4) m4[r & 3] = __builtin_fmaxf(m4[r & 3], s0.s[b][r]);
+      m4[r & 3] = __builtin_fmaxf(m4[r & 3], s1.s[b][r]);
+    }
+  const float mx = max_xor32(__builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3])));
+  if (__any((mx - m_run) * c > 8.f)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2((m_run - m_new) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+    m_run = m_new;
+  }
+  const float mc = m_run * c;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0.s[b][r] = fast_exp2(__builtin_fmaf(s0.s[b][r], c, -mc));
+      s1.s[b][r] = fast_exp2(__builtin_fmaf(s1.s[b][r], c, -mc));
+    }
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r0 = 8 * u;
+      pf0[b][u] = u32x4{pack2<T>(s0.s[b][r0 + 0], s0.s[b][r0 + 1]), pack2<T>(s0.s[b][r0 + 2], s0.s[b][r0 + 3]),
+                        pack2<T>(s0.s[b][r0 + 4], s0.s[b][r0 + 5]), pack2<T>(s0.s[b][r0 + 6], s0.s[b][r0 + 7])};
+      pf1[b][u] = u32x4{pack2<T>(s1.s[b][r0 + 0], s1.s[b][r0 + 1]), pack2<T>(s1.s[b][r0 + 2], s1.s[b][r0 + 3]),
+                        pack2<T>(s1.s[b][r0 + 4], s1.s[b][r0 + 5]), pack2<T>(s1.s[b][r0 + 6], s1.s[b][r0 + 7])};
+    }
+  float s4[4] = {s0.s[0][0], s0.s[0][1], s0.s[0][2], s0.s[0][3]};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (b > 0 || r >= 4) s4[r & 3] += s0.s[b][r];
+      s4[r & 3] += s1.s[b][r];
+    }
+  l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
+}
+
+template <typename T>
+__global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave >> 2;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int kvh = blockIdx.x % a.Hkv;
+  const int4 w0 = a.work[2 * (blockIdx.x / a.Hkv)], w1 = a.work[2 * (blockIdx.x / a.Hkv) + 1];
+  const int seq = w0.x, t0 = w0.y, qs = w0.z, nn = w0.w, cached = w1.x;
+  if (seq < 0 || w1.z <= 0) return;
+  const int len = cached + nn;
+  const int32_t* pages = a.kv_indices + w1.y;
+  const int tpw = 32 / a.G;
+  const int kv_end = w1.z;
+  const int last = kv_end - 1;
+  const int ntiles = w1.w;
+  const int npairs = (ntiles + 1) >> 1;
+
+  const int n = lane & 31, h = lane >> 5;
+  const int tok = t0 + wave * tpw + n / a.G;
+  const bool row_valid = tok < nn;
+  const int qp = row_valid ? cached + tok : len - 1;
+  const int wave_tok_hi = min(t0 + wave * tpw + tpw, nn) - 1;
+  const int wave_qp_hi = wave_tok_hi >= t0 + wave * tpw ? cached + wave_tok_hi : -1;
+  const int wave_qp_lo = cached + t0 + wave * tpw;
+  const float c = a.scale_log2;
+
+  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * 2);
+  const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
+  const unsigned rb = (unsigned)a.row_bytes;
+  const unsigned koff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * k_chunk(r0, lane);
+  const unsigned koff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * k_chunk(r1, lane);
+  const unsigned voff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * v_chunk(r0, lane);
+  const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
+  const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
+  const unsigned vread = (unsigned)(kVBase2 + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
+
+  const char* kc = reinterpret_cast<const char*>(a.kc);
+  const char* vc = reinterpret_cast<const char*>(a.vc);
+  const int g16 = 16 * (wu >> 1);
+  auto k_slot = [&](int t) { return lds + (t & (kRingK2 - 1)) * kTileBytes; };
+  auto v_slot = [&](int t) { return lds + kVBase2 + (t & (kRingV2 - 1)) * kTileBytes; };
+
+  const int* idwin = reinterpret_cast<const int*>(lds + kIdBase2) + wu * 128;
+  auto load_ids = [&](int base, int sel) {
+    dma4(reinterpret_cast<const char*>(pages), 4u * (unsigned)(min((base + lane) * kBN + g16, last) >> a.bs_shift),
+         lds_offset(idwin + 64 * sel));
+  };
+  int wbase = 0, wsel = 0;
+  auto blk_of = [&](int t) { return __builtin_amdgcn_readfirstlane(idwin[64 * wsel + t - wbase]); };
+  load_ids(0, 0);
+  auto blk_direct = [&](int t) { return pages[min(t * kBN + g16, last) >> a.bs_shift]; };
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // prologue: K(0..3), V(0..1), then Q; all of them have landed after the first barrier
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (t < ntiles) {
+      const int b = blk_direct(t);
+      dma_tile<false>(kc, a, b, t * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(t));
+      if (t < 2) dma_tile<true>(vc, a, b, t * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(t));
+    }
+  }
+  u32x4 qf[8];
+  {
+    const int head = kvh * a.G + (n % a.G);
+    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
+      qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
+               : "memory");
+  barrier_vm<0>();
+
+  STile st0, st1;
+  u32x4 pf0[2][2], pf1[2][2];
+  if (0 <= wave_qp_hi) {
+    st0 = scores<T>(lds, kread, qf);
+    if (1 < ntiles && kBN <= wave_qp_hi) st1 = scores<T>(lds, kread + kTileBytes, qf);
+    if (grp == 0) softmax_two<T>(st0, st1, pf0, pf1, oacc, m_run, l_run, 0, qp, wave_qp_lo, h, c);
+  }
+  barrier_lds();  // K(0), K(1) have been read: phase 0 loads K(4), K(5) into their slots
+
+  for (int p = 0; p < 2 * npairs; ++p) {
+    const int j = p >> 1;
+    const int ta = 2 * j;  // the pair's first tile
+    if ((p & 1) == 0) {
+      const int v0b = blk_of(ta + 2), v1b = blk_of(ta + 3), k0b = blk_of(ta + 4), k1b = blk_of(ta + 5);
+      if (ta + 7 >= wbase + 64) {  // the next even phase reads ids of tiles ta + 4 .. ta + 7
+        wsel ^= 1;
+        wbase = ta + 4;
+        load_ids(wbase, wsel);
+      }
+      if (ta + 2 < ntiles)
+        dma_tile<true>(vc, a, v0b, (ta + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 2));
+      if (ta + 3 < ntiles)
+        dma_tile<true>(vc, a, v1b, (ta + 3) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 3));
+      if (ta + 4 < ntiles)
+        dma_tile<false>(kc, a, k0b, (ta + 4) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 4));
+      if (ta + 5 < ntiles)
+        dma_tile<false>(kc, a, k1b, (ta + 5) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 5));
+    }
+    if ((p & 1) == grp) {  // matrix phase of pair j
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tv = ta + u, tk = ta + 2 + u;
+        const unsigned vb = vread + (tv & (kRingV2 - 1)) * kTileBytes, kb = kread + (tk & (kRingK2 - 1)) * kTileBytes;
+        const bool do_pv = tv < ntiles && tv * kBN <= wave_qp_hi, do_s = tk < ntiles && tk * kBN <= wave_qp_hi;
+        STile& st = u ? st1 : st0;
+        const u32x4 (&pf)[2][2] = u ? pf1 : pf0;
+        if (do_pv && do_s) {
+          matrix_phase<T>(lds, vb, kb, pf, oacc, st, qf);
+        } else {
+          if (do_pv) pv_tile<T>(lds, vb, pf, oacc);
+          if (do_s) st = scores<T>(lds, kb, qf);
+        }
+      }
+      __builtin_amdgcn_s_setprio(0);
+    } else {  // vector phase: softmax of the pair starting at tile 2 ((p + 1) >> 1)
+      const int tn = 2 * ((p + 1) >> 1);
+      if (tn < ntiles && tn * kBN <= wave_qp_hi)
+        softmax_two<T>(st0, st1, pf0, pf1, oacc, m_run, l_run, tn * kBN, qp, wave_qp_lo, h, c);
+    }
+    if (p & 1)
+      barrier_vm<0>();
+    else
+      barrier_lds();
+  }
+
+  const float inv = 1.f / l_run;
+  char* ost = lds + wave * (32 * kRowBytes);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int r = 4 * g4;
+      const u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
+                             pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
+      *reinterpret_cast<u32x2*>(ost + n * kRowBytes + 16 * ((4 * dt + g4) ^ (n & 15)) + 8 * h) = pk;
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4), chunk = lane & 15;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + row * kRowBytes + 16 * (chunk ^ (row & 15)));
+    const int rtok = t0 + wave * tpw + row / a.G;
+    if (rtok < nn) {
+      uint16_t* o = a.out + (int64_t)(qs + rtok) * a.o_st + (int64_t)(kvh * a.G + row % a.G) * a.o_sh;
+      *reinterpret_cast<u32x4*>(o + 8 * chunk) = v;
+    }
+  }
+}
 }  // namespace
 }  // namespace mllm
 
@@ -566,6 +815,13 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.o_sh = out_stride_head;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
+  if (kPrefill128 && !fp8) {
+    if (dtype == MLLM_DTYPE_BF16)
+      prefill128_kernel<BF16><<<grid, 512, 0, st>>>(a);
+    else
+      prefill128_kernel<F16><<<grid, 512, 0, st>>>(a);
+    return check_launch(fn.c_str());
+  }
   if (dtype == MLLM_DTYPE_BF16) {
     if (fp8)
       prefill_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
