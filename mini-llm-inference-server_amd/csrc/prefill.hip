@@ -299,6 +299,39 @@ __device__ __forceinline__ void matrix_phase(const char* lds, unsigned vb, unsig
   }
 }
 
+
+// Both matrix phases of a pair as one sequence of 64 MFMAs (PV(a), S(a+2), PV(a+1), S(a+3)), one operand
+// ring across it, so the second half's first operands are read while the first half's last MFMAs run.
+template <typename T>
+__device__ __forceinline__ void matrix_phase_pair(const char* lds, unsigned vb0, unsigned kb0, unsigned vb1,
+                                                  unsigned kb1, const u32x4 (&pf0)[2][2], const u32x4 (&pf1)[2][2],
+                                                  f32x16 (&oacc)[4], STile& st0, STile& st1, const u32x4 (&qf)[8]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st0.s[b][r] = st1.s[b][r] = 0.f;
+  auto operand = [&](int f) { return (f < 32) ? matrix_operand(lds, vb0, kb0, f) : matrix_operand(lds, vb1, kb1, f - 32); };
+  u32x4 ring[kLookahead + 1];
+#pragma unroll
+  for (int f = 0; f < kLookahead; ++f) ring[f] = operand(f);
+#pragma unroll
+  for (int f = 0; f < 64; ++f) {
+    if (f + kLookahead < 64) ring[(f + kLookahead) % (kLookahead + 1)] = operand(f + kLookahead);
+    const u32x4 op = ring[f % (kLookahead + 1)];
+    const int g = f & 31;
+    const u32x4 (&pf)[2][2] = f < 32 ? pf0 : pf1;
+    STile& st = f < 32 ? st0 : st1;
+    if (g < 16) {
+      const int u = g >> 2;
+      oacc[g & 3] = Mfma<T>::m32x32x16(op, pf[u >> 1][u & 1], oacc[g & 3]);
+    } else {
+      const int e = g - 16;
+      st.s[e & 1] = Mfma<T>::m32x32x16(op, qf[e >> 1], st.s[e & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Two wavefront groups of one workgroup, phase-shifted by half an iteration: while group A (waves
 // 0-3) runs its matrix phase, group B (waves 4-7) runs its vector phase, and the next barrier swaps
 // them, so each SIMD (one wave of each group) keeps its matrix pipe and its vector ALU busy together.
@@ -519,6 +552,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 // (64 MFMAs), and the vector phase runs one softmax over both score tiles (one max and one rescale
 // test per 128 keys).  Half the phases means half the barriers and per-phase bookkeeping per key:
 // prefix_64 674 us against 702-716 us for 64-key phases, mixed_128 76 against 78-80 us (same box).
+// When all four products of a pair run, they are one 64-MFMA sequence with one operand ring
+// (matrix_phase_pair), so the second tile's first operands are read under the first tile's last
+// MFMAs: another 1.3% on prefix_64 (649 against 657-659 us), bit-identical.
 // Rings: K and V four tiles each (128 KB).  Even phase 2j loads V(2j+2), V(2j+3) into the slots of
 // V(2j-2), V(2j-1) and K(2j+4), K(2j+5) into those of K(2j), K(2j+1), all freed by the barrier that
 // ended phase 2j-1; the barrier ending phase 2j+1 waits for all of them (the next phase reads them).
@@ -706,6 +742,12 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
     }
     if ((p & 1) == grp) {  // matrix phase of pair j
       __builtin_amdgcn_s_setprio(1);
+      const bool full = ta + 3 < ntiles && (ta + 3) * kBN <= wave_qp_hi;  // all four products of the pair
+      if (full) {
+        matrix_phase_pair<T>(lds, vread + (ta & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 2) & (kRingK2 - 1)) * kTileBytes,
+                             vread + ((ta + 1) & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 3) & (kRingK2 - 1)) * kTileBytes,
+                             pf0, pf1, oacc, st0, st1, qf);
+      } else
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int tv = ta + u, tk = ta + 2 + u;
