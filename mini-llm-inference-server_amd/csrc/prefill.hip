@@ -21,18 +21,18 @@
 //
 // The two halves of the workgroup run phase-shifted (see prefill_kernel): one half's matrix phase
 // coincides with the other half's softmax, so every SIMD has an MFMA stream and a vector stream at
-// once.  With 16-bit pools a phase covers two tiles (prefill128_kernel: 128 keys per phase, one
-// softmax over both score tiles); with fp8 pools one tile (prefill_kernel).  Tiles entirely above a wavefront's causal diagonal are skipped.  Keys past the workgroup's
-// last visible key are loaded as copies of that key's row (their scores are masked, so P is exactly
+// once.  A phase covers two tiles (prefill128_kernel: 128 keys per phase, one softmax over both
+// score tiles); prefill_kernel, one tile per phase, is kept as a build option.  Tiles entirely above a
+// wavefront's causal diagonal are skipped.  Keys past the workgroup's last visible key are loaded as copies of that key's row (their scores are masked, so P is exactly
 // 0 and pool slots past a row's length are never read).  The grid is 1-D with the KV head fastest,
 // so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and
 // keeps that head's shared-prefix pages in its own L2.
 //
-// fp8 (e4m3fn) pools: the DMA cannot widen, so tiles go through VGPRs instead.  At the even phase where
-// the 16-bit kernel issues its DMA, each lane loads 16 pool bytes of its wavefront's 8 tile rows; at
-// the end of the next (odd) phase it widens them to bf16/fp16 (exact) and writes them with ds_write_b128
-// into the same swizzled LDS layout, before the barrier that publishes them.  Everything downstream of
-// LDS is the 16-bit kernel; k_scale is folded into the softmax scale and v_scale into the output.
+// fp8 (e4m3fn) pools: the DMA cannot widen, so tiles go through VGPRs instead.  Each lane loads 16 pool
+// bytes of its wavefront's 8 tile rows, widens them to bf16/fp16 (exact) and writes them with
+// ds_write_b128 into the same swizzled LDS layout, before the barrier that publishes them (the phase
+// of each kernel's loads is stated there).  Everything downstream of LDS is the 16-bit path; k_scale
+// is folded into the softmax scale and v_scale into the output.
 #include <math.h>
 
 #include "common.h"
@@ -50,9 +50,7 @@ constexpr int kVBase = kRingK * kTileBytes;  // byte offset of the V ring
 constexpr int kIdBase = (kRingK + kRingV) * kTileBytes;  // per wavefront two 64-entry windows of block ids
 constexpr int kLdsBytes = kIdBase + 8 * 2 * 64 * 4;
 constexpr int kQTileRows = 256;  // query rows (token x head of the group) per workgroup: 8 waves x 32
-// 16-bit pools run prefill128_kernel (128-key phases); 0 selects prefill_kernel (64-key phases), which
-// fp8 pools always run (their tiles pass through VGPRs, and two tiles of staging do not fit beside
-// the 128-key kernel's registers)
+// 1 (default): prefill128_kernel (128-key phases) for every pool type; 0: prefill_kernel (64-key phases)
 #ifndef MLLM_PREFILL_128
 #define MLLM_PREFILL_128 1
 #endif
@@ -546,7 +544,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- 16-bit pools: 128-key phases
+// ---------------------------------------------------------------- 128-key phases
 // The same workgroup, tiles and operand layouts as prefill_kernel, but every phase covers two 64-key
 // tiles (a pair): the matrix phase of pair j runs PV of tiles 2j and 2j+1 and S of tiles 2j+2 and 2j+3
 // (64 MFMAs), and the vector phase runs one softmax over both score tiles (one max and one rescale
@@ -560,6 +558,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 // ended phase 2j-1; the barrier ending phase 2j+1 waits for all of them (the next phase reads them).
 // A pair's second tile past the row (odd tile counts) or past a wavefront's last row is skipped in the
 // matrix phase and fully masked in the softmax, so its P is 0.
+// fp8 pools: V(2j+2), V(2j+3) are loaded into VGPRs at the start of phase 2j and K(2j+4), K(2j+5) at
+// the start of phase 2j+1, each pair widened into LDS at the end of its phase (the slots are free
+// since the barrier that ended phase 2j-1).  The eight staging VGPRs leave no room for the pair's
+// single operand ring, so fp8 pools run the two tiles' products one after the other.  Against the
+// 64-key kernel on fp8 pools: prefix_64 725 against 756 us, mixed_128 82 against 87 us (same box).
 constexpr int kRingK2 = 4, kRingV2 = 4;  // K and V tiles in LDS
 constexpr int kVBase2 = kRingK2 * kTileBytes;
 constexpr int kIdBase2 = (kRingK2 + kRingV2) * kTileBytes;
@@ -627,7 +630,7 @@ __device__ __forceinline__ void softmax_two(STile& s0, STile& s1, u32x4 (&pf0)[2
   l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
 }
 
-template <typename T>
+template <typename T, bool F8>
 __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes2];
   const int tid = threadIdx.x;
@@ -656,13 +659,14 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
   const int wave_qp_lo = cached + t0 + wave * tpw;
   const float c = a.scale_log2;
 
-  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * 2);
+  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * (F8 ? 1 : 2));
   const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
   const unsigned rb = (unsigned)a.row_bytes;
   const unsigned koff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * k_chunk(r0, lane);
   const unsigned koff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * k_chunk(r1, lane);
   const unsigned voff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * v_chunk(r0, lane);
   const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
+  const unsigned soff = (unsigned)(8 * (wave & 1) + (lane >> 3)) * rb + head_bytes + 16u * (lane & 7);  // fp8
   const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
   const unsigned vread = (unsigned)(kVBase2 + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
 
@@ -689,13 +693,33 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // prologue: K(0..3), V(0..1), then Q; all of them have landed after the first barrier
+  // prologue: K(0..3), V(0..1), then Q; all of them have landed after the first barrier (fp8 pools: all
+  // six tiles loaded into registers first, then widened into LDS)
+  if constexpr (F8) {
+    u32x4 kx[4], vx[2];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (t < ntiles) {
-      const int b = blk_direct(t);
-      dma_tile<false>(kc, a, b, t * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(t));
-      if (t < 2) dma_tile<true>(vc, a, b, t * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(t));
+    for (int t = 0; t < 4; ++t) {
+      if (t < ntiles) {
+        const int b = blk_direct(t);
+        kx[t] = stage_load(kc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
+        if (t < 2) vx[t] = stage_load(vc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (t < ntiles) {
+        stage_store<T, false>(kx[t], wu, lane, k_slot(t));
+        if (t < 2) stage_store<T, true>(vx[t], wu, lane, v_slot(t));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (t < ntiles) {
+        const int b = blk_direct(t);
+        dma_tile<false>(kc, a, b, t * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(t));
+        if (t < 2) dma_tile<true>(vc, a, b, t * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(t));
+      }
     }
   }
   u32x4 qf[8];
@@ -721,28 +745,43 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
   }
   barrier_lds();  // K(0), K(1) have been read: phase 0 loads K(4), K(5) into their slots
 
+  // fp8 pools: V(2j+2), V(2j+3) pass through registers during the even phase and K(2j+4), K(2j+5) during
+  // the odd one, each widened into LDS at the end of its phase
+  u32x4 st_a = {0, 0, 0, 0}, st_b = {0, 0, 0, 0};
+  int k0b = 0, k1b = 0;
   for (int p = 0; p < 2 * npairs; ++p) {
     const int j = p >> 1;
     const int ta = 2 * j;  // the pair's first tile
     if ((p & 1) == 0) {
-      const int v0b = blk_of(ta + 2), v1b = blk_of(ta + 3), k0b = blk_of(ta + 4), k1b = blk_of(ta + 5);
+      const int v0b = blk_of(ta + 2), v1b = blk_of(ta + 3);
+      k0b = blk_of(ta + 4);
+      k1b = blk_of(ta + 5);
       if (ta + 7 >= wbase + 64) {  // the next even phase reads ids of tiles ta + 4 .. ta + 7
         wsel ^= 1;
         wbase = ta + 4;
         load_ids(wbase, wsel);
       }
-      if (ta + 2 < ntiles)
-        dma_tile<true>(vc, a, v0b, (ta + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 2));
-      if (ta + 3 < ntiles)
-        dma_tile<true>(vc, a, v1b, (ta + 3) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 3));
-      if (ta + 4 < ntiles)
-        dma_tile<false>(kc, a, k0b, (ta + 4) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 4));
-      if (ta + 5 < ntiles)
-        dma_tile<false>(kc, a, k1b, (ta + 5) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 5));
+      if constexpr (F8) {
+        if (ta + 2 < ntiles) st_a = stage_load(vc, a, v0b, (ta + 2) * kBN, last, kv_end, wu, soff, head_bytes, lane);
+        if (ta + 3 < ntiles) st_b = stage_load(vc, a, v1b, (ta + 3) * kBN, last, kv_end, wu, soff, head_bytes, lane);
+      } else {
+        if (ta + 2 < ntiles)
+          dma_tile<true>(vc, a, v0b, (ta + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 2));
+        if (ta + 3 < ntiles)
+          dma_tile<true>(vc, a, v1b, (ta + 3) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(ta + 3));
+        if (ta + 4 < ntiles)
+          dma_tile<false>(kc, a, k0b, (ta + 4) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 4));
+        if (ta + 5 < ntiles)
+          dma_tile<false>(kc, a, k1b, (ta + 5) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(ta + 5));
+      }
+    } else if constexpr (F8) {
+      if (ta + 4 < ntiles) st_a = stage_load(kc, a, k0b, (ta + 4) * kBN, last, kv_end, wu, soff, head_bytes, lane);
+      if (ta + 5 < ntiles) st_b = stage_load(kc, a, k1b, (ta + 5) * kBN, last, kv_end, wu, soff, head_bytes, lane);
     }
     if ((p & 1) == grp) {  // matrix phase of pair j
       __builtin_amdgcn_s_setprio(1);
-      const bool full = ta + 3 < ntiles && (ta + 3) * kBN <= wave_qp_hi;  // all four products of the pair
+      // all four products of the pair (fp8 pools keep two tiles of staging registers: no single ring)
+      const bool full = !F8 && ta + 3 < ntiles && (ta + 3) * kBN <= wave_qp_hi;
       if (full) {
         matrix_phase_pair<T>(lds, vread + (ta & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 2) & (kRingK2 - 1)) * kTileBytes,
                              vread + ((ta + 1) & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 3) & (kRingK2 - 1)) * kTileBytes,
@@ -768,13 +807,27 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
       if (tn < ntiles && tn * kBN <= wave_qp_hi)
         softmax_two<T>(st0, st1, pf0, pf1, oacc, m_run, l_run, tn * kBN, qp, wave_qp_lo, h, c);
     }
-    if (p & 1)
-      barrier_vm<0>();
-    else
-      barrier_lds();
+    if constexpr (F8) {  // the staged tiles' slots were freed by the barrier that ended phase 2j-1
+      if ((p & 1) == 0) {
+        if (ta + 2 < ntiles) stage_store<T, true>(st_a, wu, lane, v_slot(ta + 2));
+        if (ta + 3 < ntiles) stage_store<T, true>(st_b, wu, lane, v_slot(ta + 3));
+      } else {
+        if (ta + 4 < ntiles) stage_store<T, false>(st_a, wu, lane, k_slot(ta + 4));
+        if (ta + 5 < ntiles) stage_store<T, false>(st_b, wu, lane, k_slot(ta + 5));
+      }
+      if (p & 1)
+        barrier_vm<0>();  // also the id window loaded in the even phase
+      else
+        barrier_lds();
+    } else {
+      if (p & 1)
+        barrier_vm<0>();
+      else
+        barrier_lds();
+    }
   }
 
-  const float inv = 1.f / l_run;
+  const float inv = (F8 ? a.v_scale : 1.f) / l_run;
   char* ost = lds + wave * (32 * kRowBytes);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -857,11 +910,18 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.o_sh = out_stride_head;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
-  if (kPrefill128 && !fp8) {
-    if (dtype == MLLM_DTYPE_BF16)
-      prefill128_kernel<BF16><<<grid, 512, 0, st>>>(a);
-    else
-      prefill128_kernel<F16><<<grid, 512, 0, st>>>(a);
+  if (kPrefill128) {
+    if (dtype == MLLM_DTYPE_BF16) {
+      if (fp8)
+        prefill128_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
+      else
+        prefill128_kernel<BF16, false><<<grid, 512, 0, st>>>(a);
+    } else {
+      if (fp8)
+        prefill128_kernel<F16, true><<<grid, 512, 0, st>>>(a);
+      else
+        prefill128_kernel<F16, false><<<grid, 512, 0, st>>>(a);
+    }
     return check_launch(fn.c_str());
   }
   if (dtype == MLLM_DTYPE_BF16) {

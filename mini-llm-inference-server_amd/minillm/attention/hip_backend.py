@@ -72,9 +72,10 @@ def decode_kernel_name(kv_fp8: bool, num_heads: int, num_kv_heads: int) -> str:
 
 
 def prefill_kernel_name(kv_fp8: bool) -> str:
-    """The prefill kernel mllm_paged_prefill(_fp8) launches: 16-bit pools run phases of two 64-key tiles,
-    fp8 pools (whose tiles pass through registers to be widened) phases of one."""
-    return "prefill_kernel" if kv_fp8 else "prefill128_kernel"
+    """The prefill kernel mllm_paged_prefill(_fp8) launches: phases of two 64-key tiles for every pool type
+    (fp8 tiles pass through registers to be widened on their way into LDS)."""
+    del kv_fp8
+    return "prefill128_kernel"
 
 
 def is_fp8(pool: torch.Tensor) -> bool:
