@@ -124,12 +124,20 @@ def _kernel_case(h=8, hkv=2, bs=16, steps=None, num_blocks=64, seed=0):
     return case(h=h, hkv=hkv, bs=bs, steps=steps, num_blocks=num_blocks, seed=seed)
 
 
-@pytest.mark.parametrize("h,hkv,bs", [(8, 8, 16), (16, 8, 16), (32, 4, 16), (64, 4, 16), (32, 8, 32), (32, 8, 64)],
-                         ids=["g1", "g2", "g8", "g16", "bs32", "bs64"])
+@pytest.mark.parametrize("h,hkv,bs", [(8, 8, 16), (16, 8, 16), (32, 4, 16), (64, 4, 16), (32, 8, 32), (32, 8, 64),
+                                     (32, 8, 128), (32, 8, 256)],
+                         ids=["g1", "g2", "g8", "g16", "bs32", "bs64", "bs128", "bs256"])
 def test_group_sizes_and_blocks(hip, h, hkv, bs):
     steps = [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (17, 70), (129, 130)]
     wl = _kernel_case(h=h, hkv=hkv, bs=bs, steps=steps, num_blocks=max(64, 1100 // bs))
     _check(*fp8_step(wl, 0.02, 0.02))
+
+
+def test_prefill_group_32(hip):
+    # 32 query heads per KV head, prefill rows only (decode takes at most 16)
+    steps = [(0, 37), (40, 25), (17, 70), (300, 2), (129, 130)]
+    wl = _kernel_case(h=32, hkv=1, steps=steps, num_blocks=64, seed=7)
+    _check(*fp8_step(wl, 0.04, 0.05))
 
 
 @pytest.mark.parametrize("h,hkv", [(12, 3), (12, 6), (10, 2), (20, 4), (40, 10), (14, 2)],

@@ -255,6 +255,48 @@ def test_larger_blocks(hip, bs):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("h,hkv", [(32, 1), (64, 2)], ids=["g32", "g32-hkv2"])
+def test_prefill_group_32(hip, h, hkv):
+    # 32 query heads per KV head: decode does not take it, prefill does (one token per wavefront, 8 per
+    # q tile); rows with several new tokens only, fresh and cached, lengths not tile-aligned
+    steps = [(0, 37), (40, 25), (17, 70), (300, 2), (129, 130), (0, 9)]
+    wl = _kernel_case(h=h, hkv=hkv, steps=steps, num_blocks=64)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("bs", [128, 256])
+def test_blocks_of_several_key_tiles(hip, bs):
+    # a page of 128 or 256 tokens holds 2 or 4 of the prefill kernel's 64-key tiles and 8 or 16 of
+    # decode's 16-token tiles; rows of every kind, prefixes past one page and past several
+    steps = [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (129, 130), (700, 300), (1000, 1), (255, 2)]
+    nb = sum(-(-(c + n) // bs) for c, n in steps) + 4
+    wl = _kernel_case(h=32, hkv=8, bs=bs, steps=steps, num_blocks=nb)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_tile_and_pair_boundaries(hip):
+    # the prefill kernel runs 64-key tiles in pairs: rows whose visible keys end one before, on and one
+    # after a tile, pair and q-tile boundary (odd and even tile counts, a pair's second tile past the row
+    # or past a wavefront's last row), with 2 to 65 new tokens
+    steps = []
+    for kv_end in (63, 64, 65, 127, 128, 129, 191, 192, 193, 256, 257, 320):
+        for new in (2, 33, 64, 65):
+            if new <= kv_end:
+                steps.append((kv_end - new, new))
+    nb = sum(-(-(c + n) // 16) for c, n in steps) + 4
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=nb, seed=5)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_random_mixed_steps(hip, seed):
     # seeded random steps with every row kind (fresh and cached, one and many new tokens, lengths not
