@@ -17,7 +17,7 @@ SDPA; bf16) over all 256 rows on this host's cores (torch.set_num_threads(os.cpu
 workloads on the GPU with their own kernels' rates and the same CPU baseline:
   decode_4    4 rows (contexts 37/128/211/500 + 1): step and decode-launch time (latency-bound);
   mixed_128   8 prefill + 120 decode rows: prefill launch TFLOP/s and fraction of the bf16 peak over
-              its own launch, decode launch GB/s, and the step with both launches overlapped;
+              its own launch, decode launch GB/s, and the backend's own step (backend_step_us);
   prefix_64   64 rows over a shared 2,048-token prefix: prefill launch TFLOP/s and fraction;
   decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction;
   gemm_8192   torch.mm (hipBLASLt) on 8192^3 bf16 operands, random and zero: the MFMA rate this GPU
@@ -405,7 +405,7 @@ def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
     ks = vs = 1.0
     meta = AttentionMetadata.build([SeqStep(c, n, b) for c, n, b in wl.seqs], wl.block_size, dev)
     backend.invalidate_plan()
-    plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev)
+    plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev, fp8)
     out = torch.empty_like(q)
 
     def step(ev=None):
@@ -440,7 +440,7 @@ def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
            "dec_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0,
            "pf_ms": statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0,
            "plan": plan, "meta": meta, "tensors": (q, k, v, pool_k, pool_v)}
-    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step: prefill beside decode
+    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step (attend), no events inside
         def ostep():
             backend.append(k, v, pool_k, pool_v, meta, ks, vs)
             backend.attend(q, pool_k, pool_v, meta, out, ks, vs)
@@ -454,7 +454,7 @@ def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
             ostep()
         b.record()
         torch.cuda.synchronize()
-        res["overlap_step_ms"] = a.elapsed_time(b) / steps
+        res["backend_step_ms"] = a.elapsed_time(b) / steps
     return res
 
 
@@ -469,9 +469,9 @@ def kernel_rates(wl, r, kv_elem: int) -> dict:
         tf = wl.prefill_flops() / (r["pf_ms"] * 1e-3) / 1e12
         out.update(prefill_us=round(r["pf_ms"] * 1e3, 2), prefill_flops=wl.prefill_flops(),
                    prefill_tflops=round(tf, 1), prefill_frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
-    if "overlap_step_ms" in r:
-        out["overlapped_step_us"] = round(r["overlap_step_ms"] * 1e3, 2)
-        out["overlapped_tokens_per_s_32_layers"] = round(wl.num_tokens / (LAYERS * r["overlap_step_ms"] * 1e-3), 1)
+    if "backend_step_ms" in r:
+        out["backend_step_us"] = round(r["backend_step_ms"] * 1e3, 2)
+        out["backend_tokens_per_s_32_layers"] = round(wl.num_tokens / (LAYERS * r["backend_step_ms"] * 1e-3), 1)
     return out
 
 
@@ -566,7 +566,9 @@ def main():
                                f"attention (+ split merge); value = tokens/s scaled to {LAYERS} layers",
                    "kv_dtype": "fp8_e4m3fn (scales 1)" if fp8 else "bf16",
                    "rows": n_rows, "new_tokens": wl.num_tokens, "context_tokens": sum(wl.lens),
-                   "pages_per_split": plan.pages_per_split, "decode_items": plan.num_decode,
+                   "pages_per_split": plan.pages_per_split,
+                   "decode_plan": dict(zip(("bins", "segments", "partial_slots"),
+                                           plan.decode_work[:3].tolist() if plan.num_decode else (0, 0, 0))),
                    "prefill_items": plan.num_prefill},
         "roofline": roofline,
         "per_layer": {"tokens_per_s": round(wl.num_tokens / (step_ms * 1e-3), 1), "algorithmic_bytes": step_bytes,

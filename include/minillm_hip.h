@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define MLLM_ABI_VERSION 2
+#define MLLM_ABI_VERSION 3
 
 #define MLLM_OK 0
 #define MLLM_ERR_INVALID (-1)
@@ -126,20 +126,27 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  * Per-step work plan (the analogue of FlashInfer's plan(), which the reference runs once per step:
  * src/minillm/attention/flashinfer_backend.py:44-64).  Built on the GPU from qo_indptr / kv_indptr /
  * seq_lens (tokens per row, cached + new).
- *   decode rows (num_new == 1): split into ceil(P / pages_per_split) balanced chunks of pages; one int4
- *     work item {seq, split, num_splits, first_item} each -> decode_work[num_decode_work], largest chunk
- *     first; first_item numbers the row's chunks in sequence order (the partial slots of the merge).
- *     Sequences with more than one split also get an int4 {seq, first_item, num_splits, 0}, in sequence
- *     order -> merge_work[num_merge_work].
+ *   decode rows (num_new == 1): their pages, rows in sequence order, form one stream of T pages, cut into
+ *     nb = ceil(T / pages_per_split) bins; bin b holds pages floor(b T / nb) .. floor((b + 1) T / nb) - 1
+ *     (stream-K: one decode workgroup per bin, equal work for every wavefront).  A row's part inside a
+ *     bin is a segment.  decode_work[num_decode_work] (int4 records) receives:
+ *       [0]                       {nb, segments, partial slots, 0}
+ *       [1 + b]                   {first segment, end segment, 1 + nb, -} of bin b
+ *       [1 + nb + 2 g], [.. + 1]  segment g: {first page's index in kv_indices, pages, first page within
+ *                                 the row, row length}, {qo_indptr[seq], partial slot or -1, seq, 0}
+ *     A row cut into several segments gets consecutive partial slots, one per segment, and an int4
+ *     {seq, first slot, segments, 0}, in sequence order -> merge_work[num_merge_work]; a row inside one
+ *     bin gets slot -1 (its segment writes the output).  1 + nb + 2 segments <= num_decode_work and
+ *     segments <= nb + rows - 1; cut rows <= min(rows, nb - 1).
  *   multi-token rows: one item per tile of q_tile_tokens new tokens, 8 int32 each:
  *     {seq, first_new_token, qo_indptr[seq], new tokens of seq, cached tokens of seq, kv_indptr[seq],
  *      keys visible to the tile's last token, 64-key tiles they span} -> prefill_work[8 * num_prefill_work],
  *     across all rows in decreasing number of those tiles (the prefill kernel's work per item).
- * The caller computes the three counts from the same host facts (sequence lengths and new-token
- * counts); the kernel writes at most that many items.  A decode item is written only when its partial
- * slot (first_item + split) is below num_decode_work, and a merge item only when all of its row's slots
- * are, so a step larger than the capacities loses those rows' work but never sends the decode or merge
- * kernels past a workspace sized for num_decode_work items.  pages_per_split <= 128.
+ * The caller computes the three capacities from the same host facts (sequence lengths and new-token
+ * counts) and fills the buffers with -1 beforehand.  A step whose decode plan does not fit
+ * num_decode_work records or num_merge_work merges gets no decode work at all (the header reads nb = 0),
+ * so the decode and merge kernels never index past a workspace sized for num_decode_work partial slots.
+ * Prefill items past num_prefill_work are dropped.  pages_per_split <= 128.
  */
 int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
               int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
@@ -159,17 +166,19 @@ int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, const int3
                   int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work, int32_t num_merge_work,
                   int32_t* prefill_work, int32_t num_prefill_work, void* stream);
 
-/* Bytes of fp32 split-KV partials the decode needs for num_decode_work items (0 if none split). */
+/* Bytes of fp32 split-KV partials for num_decode_work partial slots (a plan of num_decode_work records
+ * has fewer slots than records). */
 int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim);
 
 /*
  * Paged decode attention: one new token per row, over its whole context in the pool
  * (reference src/minillm/attention/paged_torch_ref.py:47-59, decode branch; FlashInfer
- * BatchDecodeWithPagedKVCacheWrapper, flashinfer_backend.py:55-58).  Split-KV over (row, KV head,
- * page chunk) on bf16/fp16 MFMA with an fp32 online softmax.  Scale softmax_scale (1/sqrt(Dh) in the
+ * BatchDecodeWithPagedKVCacheWrapper, flashinfer_backend.py:55-58).  One workgroup per (bin of the plan,
+ * KV-head group) streams the bin's row segments on bf16/fp16 MFMA with an fp32 online softmax; the grid
+ * covers (num_decode_work - 1) / 3 bins, and workgroups past the plan's own exit at once.  Scale softmax_scale (1/sqrt(Dh) in the
  * reference); query head h reads KV head h / (H / Hkv).
  * q/out: [N, H, Dh] with element strides (tok, head), unit stride on Dh; only the rows of decode
- * sequences are read and written.  A row with one chunk gets its output here; a row with several
+ * sequences are read and written.  A row inside one bin gets its output here; a row cut across bins
  * writes fp32 partials (m, l, acc) into the workspace, which mllm_merge_splits then combines, so the
  * two calls go back to back on one stream.  head_dim 128, block_size a multiple of 16,
  * H / Hkv <= 16, dtype F16 or BF16; num_merge_work (from mllm_plan) only sizes the workspace check.
@@ -199,8 +208,8 @@ int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t
  * device array of this library instead of a caller workspace: each GPU the library runs on holds its
  * own copy until the process ends, looked up on the first call on that device (the current device;
  * the stream must belong to it).  A step whose partials need more
- * (mllm_decode_workspace_bytes(num_decode_work, H, Dh) > 64 MiB when num_merge_work > 0; 4,032 items at
- * H = 32, Dh = 128) is rejected with MLLM_ERR_INVALID.  Calls that overlap on one GPU (other streams or
+ * (mllm_decode_workspace_bytes(num_decode_work, H, Dh) > 64 MiB when num_merge_work > 0; 4,032 plan
+ * records at H = 32, Dh = 128) is rejected with MLLM_ERR_INVALID.  Calls that overlap on one GPU (other streams or
  * threads) share the array and race; calls in order on one stream do not.  Arguments and results are
  * mllm_paged_decode's and mllm_merge_splits' (16-bit pools), bit for bit.
  */

@@ -1,8 +1,10 @@
 // Split-KV paged decode attention on gfx950 MFMA (reference src/minillm/attention/paged_torch_ref.py:47-59:
 // one new token per row, softmax(q K^T / sqrt(Dh)) V over the row's whole context).
 //
-// Work: one wavefront per (work item, KV head); a work item is a chunk of up to C pages of one row
-// (mllm_plan).  The wavefront streams its pages 16 tokens at a time straight from HBM into VGPRs:
+// Work: one wavefront per (bin, KV head).  The plan (mllm_plan) cuts the step's decode pages, rows in
+// sequence order, into equal bins of at most C pages; a bin holds one or more row segments.  The
+// wavefront streams its bin's pages 16 tokens at a time straight from HBM into VGPRs, across segment
+// boundaries without a pause:
 //   S^T[16 tok x 16] = K[16 tok x 128] . Q^T[128 x 16]      4 x v_mfma_f32_16x16x32 (bf16/f16)
 //   O^T[128 x 16]   += V^T[128 x 16 tok] . P^T[16 tok x 16]  8 x v_mfma_f32_16x16x16
 // The 16 MFMA columns hold the G = H / Hkv query heads that share the KV head (4 for Llama-3.1-8B);
@@ -12,8 +14,8 @@
 // Each lane loads K row (l % 16) in four 16-byte pieces and V rows 4 (l / 16) .. +3 at dims
 // 8 (l % 16) .. +7, so every wave-wide V load reads four whole 256-byte rows; the V^T operand is then
 // assembled with v_perm_b32.  The next 16-token tile is loaded before the current one is consumed.
-// Rows with one chunk write the normalised output; longer rows write fp32 (m, l, acc) partials that a
-// second kernel merges with a log-sum-exp.
+// A row that lies in one bin gets its normalised output from that segment; a row cut across bins gets
+// fp32 (m, l, acc) partials, one per segment, that a second kernel merges with a log-sum-exp.
 //
 // fp8 (e4m3fn) pools with an even number of KV heads and at most 8 query heads per KV head run
 // decode_pair_kernel (below): two KV heads per wavefront, loaded with the 16-bit kernel's shapes.  Other
@@ -59,8 +61,7 @@ struct DecodeArgs {
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
   const int32_t* seq_lens;
-  const int4* work;
-  int C;
+  const int4* work;  // the plan's decode bins and segments
   float scale_log2;  // softmax scale x k_scale x log2(e)
   float v_scale;     // output scale of an fp8 pool
   uint16_t* out;
@@ -204,117 +205,150 @@ __device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4
   }
 }
 
-// PF: tiles loaded ahead of the one being consumed (a ring of PF + 1 register tiles).
-template <typename T, bool F8, int PF, bool NT, int OCC>
+// The records of one segment of a bin (the plan's layout): r0 = {first page in kv_indices, pages, first
+// page within the row, row length}, r1 = {q row, partial slot or -1, sequence, 0}.
+struct SegRec {
+  int4 r0, r1;
+};
+__device__ __forceinline__ SegRec seg_rec(const int4* segs, int g) { return SegRec{segs[2 * g], segs[2 * g + 1]}; }
+
+// One wavefront per (bin, KV head) streams the bin's segments back to back, one 16-token tile ahead.
+// While a segment streams, the wavefront already holds the next segment's records (read one segment
+// earlier), loads its page ids and q, and reads the records of the segment after it; the lookahead
+// load of a segment's last tile fetches the next segment's first tile.  So the stream does not stop at
+// a row boundary: a new segment costs its finalisation (output or partial stores) and a fresh
+// online-softmax state.
+template <typename T, bool F8, bool NT, int OCC>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_kernel(
     const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
-  // the KV-head group varies fastest, so the workgroups of one item (adjacent heads of the same
-  // pages) run side by side
+  // the KV-head group varies fastest, so the workgroups of one bin (adjacent heads of the same pages)
+  // run side by side
   const int hg = blockIdx.x % a.HG;
-  const int item = blockIdx.x / a.HG;
+  const int bin = blockIdx.x / a.HG;
   const int kvh = hg * kWaves + (threadIdx.x >> 6);
   if (kvh >= a.Hkv) return;  // wave-uniform
-  const int4 w = a.work[item];
-  const int seq = w.x, split = w.y, nsplit = w.z, slot = w.w;
-  if (seq < 0) return;  // unfilled plan slot (the host pre-fills the plan with -1)
-  const int pg0 = a.kv_indptr[seq];
-  const int npg = a.kv_indptr[seq + 1] - pg0;
-  const int len = a.seq_lens[seq];
-  // balanced split: pages [split * P / ns, (split + 1) * P / ns)
-  const int pb = pg0 + (int)(((int64_t)split * npg) / nsplit);
-  const int pe = pg0 + (int)(((int64_t)(split + 1) * npg) / nsplit);
-  const int tok0 = (pb - pg0) * a.bs;
-  const int tok1 = min(len, (pe - pg0) * a.bs);
-  const int ntiles = (tok1 - tok0 + 15) >> 4;
+  // the header and the bin's record load together (the record carries the segments' base): the
+  // grid covers the plan's capacity, and workgroups past the step's nbins bins exit
+  const int nbins = a.work[0].x;
+  const int4 bw = a.work[1 + bin];
+  if (bin >= nbins) return;
+  const int4* segs = a.work + bw.z;
   const int tpp = a.bs >> 4;
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int qtok = a.qo_indptr[seq];
-
-  // the split's page ids, one per lane (pages 0-63 and 64-127 of the split)
-  const int page_lo = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
-  const int page_hi = lane + 64 < (pe - pb) ? a.kv_indices[pb + 64 + lane] : 0;
-
-  // B operand of S^T = K Q^T: lane (c, g) holds q head c of the group at dims 32 kk + 8 g .. +7.
-  const bool qvalid = c < a.G;
-  u32x4 qf[4];
-  {
-    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qtok * a.q_st +
-                                                   (int64_t)(kvh * a.G + (qvalid ? c : 0)) * a.q_sh);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      u32x4 v = ld16(qp + 2 * qk_dim0<F8>(kk, g));
-      qf[kk] = qvalid ? v : u32x4{0, 0, 0, 0};
-    }
-  }
-
+  const bool qvalid = c < a.G;  // lane column c is query head c of the group
   constexpr int kElem = F8 ? 1 : 2;  // pool bytes per element
   const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim * kElem;
   const int64_t blk_stride = (int64_t)a.bs * tok_stride;
   const char* kbase = a.kc + kvh * kHeadDim * kElem;
   const char* vbase = a.vc + kvh * kHeadDim * kElem;
+  const int qhead = kvh * a.G + (qvalid ? c : 0);
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 o[8];
+  // B operand of S^T = K Q^T: lane (c, g) holds q head c of the group at the dims qk_dim0 gives
+  auto load_q = [&](int qrow, u32x4 (&qf)[4]) {
+    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qrow * a.q_st + (int64_t)qhead * a.q_sh);
 #pragma unroll
-  for (int m = 0; m < 8; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int R = PF + 1;
-  TileRegs<F8> ring[R];
-  LoadCursor next;
-#pragma unroll
-  for (int r = 0; r < PF; ++r)
-    if (r < ntiles) {
-      load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[r]);
-      next.advance(tpp);
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 v = ld16(qp + 2 * qk_dim0<F8>(kk, g));
+      qf[kk] = qvalid ? v : u32x4{0, 0, 0, 0};
     }
-  for (int t0 = 0; t0 < ntiles; t0 += R) {
+  };
+  // the segment's page ids, one per lane (pages 0-63 and 64-127 of the segment)
+  auto load_pages = [&](const int4& r0, int& lo, int& hi) {
+    lo = lane < r0.y ? a.kv_indices[r0.x + lane] : 0;
+    hi = lane + 64 < r0.y ? a.kv_indices[r0.x + 64 + lane] : 0;
+  };
+
+  int gi = bw.x;
+  SegRec cur = seg_rec(segs, gi);
+  SegRec nxt = gi + 1 < bw.y ? seg_rec(segs, gi + 1) : SegRec{};
+  int page_lo, page_hi;
+  load_pages(cur.r0, page_lo, page_hi);
+  u32x4 qf[4];
+  load_q(cur.r1.x, qf);
+  TileRegs<F8> tile, ahead;  // the tile being consumed, the one loaded ahead of it
+  LoadCursor at;
+  load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+  at.advance(tpp);
+
+  while (true) {
+    const bool has_next = gi + 1 < bw.y;
+    const int tok0 = cur.r0.z * a.bs, len = cur.r0.w;
+    // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
+    // only such pages has none
+    const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
+    int next_lo = 0, next_hi = 0;
+    u32x4 next_q[4] = {};
+    SegRec after = {};
+    if (has_next) {
+      load_pages(nxt.r0, next_lo, next_hi);
+      load_q(nxt.r1.x, next_q);
+      if (gi + 2 < bw.y) after = seg_rec(segs, gi + 2);
+    }
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 o[8];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int t = t0 + r;
-      if (t < ntiles) {
-        if (t + PF < ntiles) {
-          load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g,
-                            ring[(r + PF) % R]);
-          next.advance(tpp);
+    for (int m = 0; m < 8; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bool next_loaded = false;  // the next segment's first tile is on its way into `tile`
+    for (int t = 0; t < ntiles; ++t) {
+      if (t + 1 < ntiles) {
+        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, ahead);
+        at.advance(tpp);
+      } else if (has_next) {
+        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, next_lo, next_hi, LoadCursor{}, c, g, ahead);
+        next_loaded = true;
+      }
+      if constexpr (F8) {
+        u32x4 ka[4], va[4];
+        widen<T>(tile, ka, va);
+        consume_tile<T>(ka, va, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+      } else {
+        consume_tile<T>(tile.k, tile.v, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+      }
+      tile = ahead;
+    }
+
+    if (qvalid) {
+      const int head = kvh * a.G + c;
+      const int slot = cur.r1.y;
+      // lane (c, g) owns dims 32 g + 8 i + m of head c: o[m][i]
+      if (slot < 0) {  // the row's only segment: the normalised output
+        const float inv = F8 ? a.v_scale / l_run : 1.f / l_run;
+        char* op = reinterpret_cast<char*>(a.out + (int64_t)cur.r1.x * a.o_st + (int64_t)head * a.o_sh + 32 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          u32x4 pk = u32x4{pack2<T>(o[0][i] * inv, o[1][i] * inv), pack2<T>(o[2][i] * inv, o[3][i] * inv),
+                           pack2<T>(o[4][i] * inv, o[5][i] * inv), pack2<T>(o[6][i] * inv, o[7][i] * inv)};
+          st16(op + 16 * i, pk);
         }
+      } else {
+        const int64_t row = (int64_t)slot * a.H + head;
+        float* po = a.part_o + row * kHeadDim + 32 * g;
         if constexpr (F8) {
-          u32x4 ka[4], va[4];
-          widen<T>(ring[r], ka, va);
-          consume_tile<T>(ka, va, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
-        } else {
-          consume_tile<T>(ring[r].k, ring[r].v, qf, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+#pragma unroll
+          for (int m = 0; m < 8; ++m) o[m] *= a.v_scale;
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          *reinterpret_cast<f32x4*>(po + 8 * i) = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
+          *reinterpret_cast<f32x4*>(po + 8 * i + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+        }
+        if (g == 0) a.part_ml[row] = make_float2(m_run, l_run);
       }
     }
-  }
-
-  if (!qvalid) return;
-  const int head = kvh * a.G + c;
-  // lane (c, g) owns dims 32 g + 8 i + m of head c: o[m][i]
-  if (nsplit == 1) {
-    const float inv = F8 ? a.v_scale / l_run : 1.f / l_run;
-    char* op = reinterpret_cast<char*>(a.out + (int64_t)qtok * a.o_st + (int64_t)head * a.o_sh + 32 * g);
+    if (!has_next) break;
+    ++gi;
+    cur = nxt;
+    nxt = after;
+    page_lo = next_lo;
+    page_hi = next_hi;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      u32x4 pk = u32x4{pack2<T>(o[0][i] * inv, o[1][i] * inv), pack2<T>(o[2][i] * inv, o[3][i] * inv),
-                       pack2<T>(o[4][i] * inv, o[5][i] * inv), pack2<T>(o[6][i] * inv, o[7][i] * inv)};
-      st16(op + 16 * i, pk);
-    }
-  } else {
-    const int64_t row = (int64_t)slot * a.H + head;
-    float* po = a.part_o + row * kHeadDim + 32 * g;
-    if constexpr (F8) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) o[m] *= a.v_scale;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<f32x4*>(po + 8 * i) = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
-      *reinterpret_cast<f32x4*>(po + 8 * i + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
-    }
-    if (g == 0) a.part_ml[row] = make_float2(m_run, l_run);
+    for (int kk = 0; kk < 4; ++kk) qf[kk] = next_q[kk];
+    at = LoadCursor{};
+    if (!next_loaded)  // this segment had no tile to load it behind
+      load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+    at.advance(tpp);  // the new segment's first tile is in `tile`
   }
 }
 
@@ -406,113 +440,143 @@ __device__ __forceinline__ void consume_pair(PairTile& r, const u32x4 (&qa)[4], 
   }
 }
 
-template <typename T, int W, int PF, bool NT, int OCC>
+template <typename T, int W, bool NT, int OCC>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_pair_kernel(
     const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
-  // a workgroup of W wavefronts covers 2 W KV heads of one item; HG = ceil(Hkv / (2 W)) groups per item
+  // a workgroup of W wavefronts covers 2 W KV heads of one bin; HG = ceil(Hkv / (2 W)) groups per bin
   const int hg = blockIdx.x % a.HG;
-  const int item = blockIdx.x / a.HG;
+  const int bin = blockIdx.x / a.HG;
   const int kvh0 = 2 * (hg * W + (threadIdx.x >> 6));
   if (kvh0 >= a.Hkv) return;  // wave-uniform
-  const int4 w = a.work[item];
-  const int seq = w.x, split = w.y, nsplit = w.z, slot = w.w;
-  if (seq < 0) return;  // unfilled plan slot
-  const int pg0 = a.kv_indptr[seq];
-  const int npg = a.kv_indptr[seq + 1] - pg0;
-  const int len = a.seq_lens[seq];
-  const int pb = pg0 + (int)(((int64_t)split * npg) / nsplit);
-  const int pe = pg0 + (int)(((int64_t)(split + 1) * npg) / nsplit);
-  const int tok0 = (pb - pg0) * a.bs;
-  const int tok1 = min(len, (pe - pg0) * a.bs);
-  const int ntiles = (tok1 - tok0 + 15) >> 4;
+  const int nbins = a.work[0].x;
+  const int4 bw = a.work[1 + bin];
+  if (bin >= nbins) return;
+  const int4* segs = a.work + bw.z;
   const int tpp = a.bs >> 4;
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int qtok = a.qo_indptr[seq];
-  const int page_lo = lane < (pe - pb) ? a.kv_indices[pb + lane] : 0;
-  const int page_hi = lane + 64 < (pe - pb) ? a.kv_indices[pb + 64 + lane] : 0;
 
   // column c: query head 2j G + c (head A's for c < G, head B's for G <= c < 2G); k-step t of a head
   // covers its dims 64 (t >> 1) + 16 g + 8 (t & 1) .. +7
   const bool qvalid = c < 2 * a.G;
   const bool in_b = c >= a.G;
-  u32x4 qa[4], qb[4];
-  {
-    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qtok * a.q_st +
-                                                   (int64_t)(kvh0 * a.G + (qvalid ? c : 0)) * a.q_sh);
+  const int qhead = kvh0 * a.G + (qvalid ? c : 0);
+  auto load_q = [&](int qrow, u32x4 (&qv)[4]) {
+    const char* qp = reinterpret_cast<const char*>(a.q + (int64_t)qrow * a.q_st + (int64_t)qhead * a.q_sh);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) qv[t] = ld16(qp + 2 * (64 * (t >> 1) + 16 * g + 8 * (t & 1)));
+  };
+  auto split_q = [&](const u32x4 (&qv)[4], u32x4 (&qa)[4], u32x4 (&qb)[4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const u32x4 v = ld16(qp + 2 * (64 * (t >> 1) + 16 * g + 8 * (t & 1)));
       const u32x4 z = u32x4{0, 0, 0, 0};
-      qa[t] = qvalid && !in_b ? v : z;
-      qb[t] = qvalid && in_b ? v : z;
+      qa[t] = qvalid && !in_b ? qv[t] : z;
+      qb[t] = qvalid && in_b ? qv[t] : z;
     }
-  }
+  };
+  auto load_pages = [&](const int4& r0, int& lo, int& hi) {
+    lo = lane < r0.y ? a.kv_indices[r0.x + lane] : 0;
+    hi = lane + 64 < r0.y ? a.kv_indices[r0.x + 64 + lane] : 0;
+  };
 
   const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;  // one byte per element
   const int64_t blk_stride = (int64_t)a.bs * tok_stride;
   const char* kbase = a.kc + kvh0 * kHeadDim;
   const char* vbase = a.vc + kvh0 * kHeadDim;
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 o[16];
-#pragma unroll
-  for (int m = 0; m < 16; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int R = PF + 1;
-  PairTile ring[R];
-  LoadCursor next;
-#pragma unroll
-  for (int r = 0; r < PF; ++r)
-    if (r < ntiles) {
-      load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[r]);
-      next.advance(tpp);
-    }
-  for (int t0 = 0; t0 < ntiles; t0 += R) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int t = t0 + r;
-      if (t < ntiles) {
-        if (t + PF < ntiles) {
-          load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, next, c, g, ring[(r + PF) % R]);
-          next.advance(tpp);
-        }
-        consume_pair<T>(ring[r], qa, qb, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
-      }
-    }
+  int gi = bw.x;
+  SegRec cur = seg_rec(segs, gi);
+  SegRec nxt = gi + 1 < bw.y ? seg_rec(segs, gi + 1) : SegRec{};
+  int page_lo, page_hi;
+  load_pages(cur.r0, page_lo, page_hi);
+  u32x4 qa[4], qb[4];
+  {
+    u32x4 qv[4];
+    load_q(cur.r1.x, qv);
+    split_q(qv, qa, qb);
   }
+  PairTile tile, ahead;
+  LoadCursor at;
+  load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+  at.advance(tpp);
 
-  // lanes that hold kept rows: head A's columns in lane groups 0-1, head B's in 2-3
-  if (!qvalid || in_b != (g >= 2)) return;
-  const int head = kvh0 * a.G + c;
-  const int d0 = 64 * (g & 1);  // o[m][i] is dim d0 + 16 i + m
-  if (nsplit == 1) {
-    const float inv = a.v_scale / l_run;
-    char* op = reinterpret_cast<char*>(a.out + (int64_t)qtok * a.o_st + (int64_t)head * a.o_sh + d0);
+  while (true) {
+    const bool has_next = gi + 1 < bw.y;
+    const int tok0 = cur.r0.z * a.bs, len = cur.r0.w;
+    // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
+    // only such pages has none
+    const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
+    int next_lo = 0, next_hi = 0;
+    u32x4 next_q[4] = {};
+    SegRec after = {};
+    if (has_next) {
+      load_pages(nxt.r0, next_lo, next_hi);
+      load_q(nxt.r1.x, next_q);
+      if (gi + 2 < bw.y) after = seg_rec(segs, gi + 2);
+    }
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 o[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int m = 0; m < 16; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bool next_loaded = false;  // the next segment's first tile is on its way into `tile`
+    for (int t = 0; t < ntiles; ++t) {
+      if (t + 1 < ntiles) {
+        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, ahead);
+        at.advance(tpp);
+      } else if (has_next) {
+        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, next_lo, next_hi, LoadCursor{}, c, g, ahead);
+        next_loaded = true;
+      }
+      consume_pair<T>(tile, qa, qb, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
+      tile = ahead;
+    }
+
+    // lanes that hold kept rows: head A's columns in lane groups 0-1, head B's in 2-3
+    if (qvalid && in_b == (g >= 2)) {
+      const int head = kvh0 * a.G + c;
+      const int d0 = 64 * (g & 1);  // o[m][i] is dim d0 + 16 i + m
+      const int slot = cur.r1.y;
+      if (slot < 0) {
+        const float inv = a.v_scale / l_run;
+        char* op = reinterpret_cast<char*>(a.out + (int64_t)cur.r1.x * a.o_st + (int64_t)head * a.o_sh + d0);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int m = 8 * h;
-        const u32x4 pk = u32x4{pack2<T>(o[m][i] * inv, o[m + 1][i] * inv), pack2<T>(o[m + 2][i] * inv, o[m + 3][i] * inv),
-                               pack2<T>(o[m + 4][i] * inv, o[m + 5][i] * inv), pack2<T>(o[m + 6][i] * inv, o[m + 7][i] * inv)};
-        st16(op + 2 * (16 * i + m), pk);
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int m = 8 * h;
+            const u32x4 pk =
+                u32x4{pack2<T>(o[m][i] * inv, o[m + 1][i] * inv), pack2<T>(o[m + 2][i] * inv, o[m + 3][i] * inv),
+                      pack2<T>(o[m + 4][i] * inv, o[m + 5][i] * inv), pack2<T>(o[m + 6][i] * inv, o[m + 7][i] * inv)};
+            st16(op + 2 * (16 * i + m), pk);
+          }
+        }
+      } else {
+        const int64_t row = (int64_t)slot * a.H + head;
+        float* po = a.part_o + row * kHeadDim + d0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int m = 4 * q4;
+            *reinterpret_cast<f32x4*>(po + 16 * i + m) =
+                f32x4{o[m][i] * a.v_scale, o[m + 1][i] * a.v_scale, o[m + 2][i] * a.v_scale, o[m + 3][i] * a.v_scale};
+          }
+        }
+        if ((g & 1) == 0) a.part_ml[row] = make_float2(m_run, l_run);
       }
     }
-  } else {
-    const int64_t row = (int64_t)slot * a.H + head;
-    float* po = a.part_o + row * kHeadDim + d0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int m = 4 * q4;
-        *reinterpret_cast<f32x4*>(po + 16 * i + m) =
-            f32x4{o[m][i] * a.v_scale, o[m + 1][i] * a.v_scale, o[m + 2][i] * a.v_scale, o[m + 3][i] * a.v_scale};
-      }
-    }
-    if ((g & 1) == 0) a.part_ml[row] = make_float2(m_run, l_run);
+    if (!has_next) break;
+    ++gi;
+    cur = nxt;
+    nxt = after;
+    page_lo = next_lo;
+    page_hi = next_hi;
+    split_q(next_q, qa, qb);
+    at = LoadCursor{};
+    if (!next_loaded)  // this segment had no tile to load it behind
+      load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+    at.advance(tpp);
   }
 }
 
@@ -562,46 +626,31 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
   out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = cvt1<T>(acc / lsum);
 }
 
-// Tuned on MI355X (decode_256 workload): one tile of lookahead with non-temporal K/V loads at 3
-// wavefronts per SIMD streams at 6.2 TB/s, the same as a two-tile lookahead at 2 per SIMD; forcing 4
-// per SIMD spills.
-#ifndef MLLM_DECODE_PREFETCH
-#define MLLM_DECODE_PREFETCH 1
-#endif
+// Occupancy, tuned on MI355X (decode_256): every kernel loads one 16-token tile ahead of the one it
+// consumes.  The 16-bit kernel runs 3 wavefronts per SIMD (4 spills).  With per-row splits, one tile
+// of lookahead at 3 per SIMD streamed as fast as two at 2 per SIMD, and the fp8 pair kernel ran the same
+// with one tile ahead as with two (192-195 us); the fp8 one-head kernel then ran 198 us with four tiles
+// ahead at 2 per SIMD against 205 us with one at 4.
 #ifndef MLLM_DECODE_OCC
 #define MLLM_DECODE_OCC 3
 #endif
-constexpr int kPrefetch = MLLM_DECODE_PREFETCH;
 constexpr bool kNonTemporal = true;
 constexpr int kOccupancy = MLLM_DECODE_OCC;
-// One-head fp8 kernel: fp8 tiles hold half the bytes in half the registers, and widening them adds VALU work per byte: four
-// tiles of lookahead at 2 wavefronts per SIMD (171 VGPRs, no spill) measured 198.3-198.7 us on
-// decode_256 (5.62-5.63 TB/s), against 203-204 us for 3 tiles at 3 per SIMD, 205 us for 1 at 4 and
-// 213 us for 2 at 3 (same box, alternating); 5 and 6 tiles at 2 per SIMD match 4, 8 is 1% slower.
-#ifndef MLLM_DECODE_FP8_PREFETCH
-#define MLLM_DECODE_FP8_PREFETCH 4
-#endif
-constexpr int kPrefetchFp8 = MLLM_DECODE_FP8_PREFETCH;
 #ifndef MLLM_DECODE_FP8_OCC
 #define MLLM_DECODE_FP8_OCC 2
 #endif
 constexpr int kOccupancyFp8 = MLLM_DECODE_FP8_OCC;
 
-// The pair kernel (fp8, two KV heads per wavefront): W wavefronts per workgroup, PF tiles of lookahead at
-// OCC wavefronts per SIMD.  On decode_256: 4 / 2 / 2 (221 VGPRs) 192-195 us; 4 / 1 / 2 the same; 2 per
-// workgroup 199-204 us and 1 per workgroup 212-214 us (a workgroup on all 8 KV heads reads whole pages);
-// the one-head kernel 198 us on the same box.
+// The pair kernel (fp8, two KV heads per wavefront): W wavefronts per workgroup at OCC wavefronts per
+// SIMD.  With per-row splits on decode_256: 4 per workgroup 192-195 us, 2 per workgroup 199-204 us and 1
+// per workgroup 212-214 us (a workgroup on all 8 KV heads reads whole pages).
 #ifndef MLLM_DECODE_PAIR_WAVES
 #define MLLM_DECODE_PAIR_WAVES 4
 #endif
 constexpr int kWavesPair = MLLM_DECODE_PAIR_WAVES;
-#ifndef MLLM_DECODE_PAIR_PREFETCH
-#define MLLM_DECODE_PAIR_PREFETCH 2
-#endif
 #ifndef MLLM_DECODE_PAIR_OCC
 #define MLLM_DECODE_PAIR_OCC 2
 #endif
-constexpr int kPrefetchPair = MLLM_DECODE_PAIR_PREFETCH;
 constexpr int kOccupancyPair = MLLM_DECODE_PAIR_OCC;
 
 // fp8 pools run the pair kernel when the KV heads pair up and a pair's query heads fit 16 columns.
@@ -609,20 +658,23 @@ __host__ __device__ constexpr bool pair_heads(int num_kv_heads, int group) {
   return num_kv_heads % 2 == 0 && 2 * group <= 16;
 }
 
+// Bins a plan of n_work records can hold: a header, then per bin one record and at least one segment
+// of two records.  The grid covers that many bins; the workgroups past the step's own exit at once.
+constexpr int max_bins(int n_work) { return n_work >= 4 ? (n_work - 1) / 3 : 0; }
+
 template <typename T, bool F8>
 int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
+  const unsigned bins = (unsigned)max_bins(n_work);
+  if (bins == 0) return MLLM_OK;
   if constexpr (F8) {
     if (pair_heads(a.Hkv, a.G)) {
       DecodeArgs b = a;
       b.HG = (a.Hkv + 2 * kWavesPair - 1) / (2 * kWavesPair);
-      decode_pair_kernel<T, kWavesPair, kPrefetchPair, kNonTemporal, kOccupancyPair>
-          <<<(unsigned)n_work * (unsigned)b.HG, 64 * kWavesPair, 0, st>>>(b);
+      decode_pair_kernel<T, kWavesPair, kNonTemporal, kOccupancyPair><<<bins * (unsigned)b.HG, 64 * kWavesPair, 0, st>>>(b);
       return check_launch("mllm_paged_decode_fp8");
     }
   }
-  const unsigned grid = (unsigned)n_work * (unsigned)a.HG;
-  decode_kernel<T, F8, F8 ? kPrefetchFp8 : kPrefetch, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy>
-      <<<grid, 64 * kWaves, 0, st>>>(a);
+  decode_kernel<T, F8, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy><<<bins * (unsigned)a.HG, 64 * kWaves, 0, st>>>(a);
   return check_launch(F8 ? "mllm_paged_decode_fp8" : "mllm_paged_decode");
 }
 
@@ -689,7 +741,6 @@ int paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   a.kv_indices = kv_indices;
   a.seq_lens = seq_lens;
   a.work = reinterpret_cast<const int4*>(decode_work);
-  a.C = pages_per_split;
   a.scale_log2 = softmax_scale * k_scale * kLog2e;
   a.v_scale = v_scale;
   a.out = static_cast<uint16_t*>(out);
@@ -814,7 +865,7 @@ int scratch_ptr(void** out) {
   return MLLM_OK;
 }
 
-// Decode items whose partials fit in the scratch.
+// Plan records (partial slots) whose partials fit in the scratch.
 int64_t noalloc_max_work(int32_t num_heads, int32_t head_dim) {
   const int64_t per = mllm_decode_workspace_bytes(1, num_heads, head_dim);
   return per > 0 ? kScratchBytes / per : 0;
@@ -839,7 +890,7 @@ extern "C" int mllm_paged_decode_noalloc(const void* q, int64_t q_stride_tok, in
                "mllm_paged_decode_noalloc: the step's split partials need " + std::to_string(need) +
                    " bytes, more than the " + std::to_string(kScratchBytes) + "-byte scratch (at most " +
                    std::to_string(noalloc_max_work(num_heads, head_dim)) +
-                   " decode items when rows are split); use mllm_paged_decode with a workspace");
+                   " plan records when rows are cut); use mllm_paged_decode with a workspace");
   MLLM_REQUIRE(num_merge_work == 0 || merge_work, MLLM_ERR_INVALID, "mllm_paged_decode_noalloc: null merge_work");
   if (num_decode_work == 0) return MLLM_OK;
   void* ws = nullptr;

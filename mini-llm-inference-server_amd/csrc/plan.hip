@@ -1,11 +1,14 @@
 // Per-step work plan, built on the GPU once per step and reused by every layer (the role of
 // FlashInfer's plan(), reference src/minillm/attention/flashinfer_backend.py:44-64).
 //
-// One workgroup scans the S sequences: a decode row (one new token) of P pages becomes ns = ceil(P / C)
-// split-KV items of P / ns pages each (balanced); a row with several new tokens becomes ceil(new / q_tile)
-// prefill items.  Both lists are launched longest first (counting sorts: decode items on their size in
-// pages, prefill items on the 64-key tiles their causal context spans), so the short items fill the tail
-// of each launch.  An exclusive scan gives each decoded row its canonical partial slots.
+// One workgroup scans the S sequences.
+// Decode rows (one new token): their pages, in sequence order, form one stream of T pages, cut into
+// nb = ceil(T / C) bins of floor or ceil(T / nb) pages (stream-K).  One decode workgroup streams one bin,
+// so every wavefront of the launch gets the same number of pages and the launch is one round of equal
+// work, whatever the rows' lengths.  A row's part inside a bin is a segment; a row cut into several
+// segments writes fp32 partials, one slot per segment, that the merge combines.
+// Rows with several new tokens: ceil(new / q_tile) prefill items, launched longest first (a counting
+// sort on the 64-key tiles each item's causal context spans), so the short items fill the tail.
 #include "common.h"
 
 namespace mllm {
@@ -51,6 +54,15 @@ __device__ __forceinline__ int prefill_class(int cached, int t0, int nn, int q_t
   return min(max((kv_end + kPrefillKeyTile - 1) / kPrefillKeyTile, 0), kPrefillClasses - 1);
 }
 
+// Bin of page p of the step's decode page stream: B(b) <= p < B(b + 1), B(b) = floor(b T / nb).  The
+// quotient floor(p nb / T) is that bin or the one before it (every bin holds at least one page: nb <= T).
+__device__ __forceinline__ int64_t bin_start(int64_t b, int64_t total, int64_t nb) { return b * total / nb; }
+__device__ __forceinline__ int bin_of(int64_t p, int64_t total, int nb) {
+  int b = (int)(p * nb / total);
+  if (b + 1 < nb && bin_start(b + 1, total, nb) <= p) ++b;
+  return b;
+}
+
 // split_dev: when not null, the split size is read from device memory (clamped to [pages_per_split, 128]:
 // the capacities were sized for pages_per_split, so no item is ever dropped).
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ qo_indptr,
@@ -62,39 +74,25 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
                                                             int4* __restrict__ merge_work, int32_t cap_merge,
                                                             int4* __restrict__ prefill_work, int32_t cap_prefill) {
   __shared__ int sums[kPlanThreads / 64];
-  __shared__ int hist[kMaxSplitPages + 1];  // decode items per size in pages
-  __shared__ int offs[kMaxSplitPages + 1];  // next free position of each size class
-  __shared__ int phist[kPrefillClasses];    // prefill items per size class (tiles, capped)
+  __shared__ int phist[kPrefillClasses];  // prefill items per size class (tiles, capped)
+  __shared__ unsigned long long s_pages;  // decode pages of the step
   const int pages_per_split =
       split_dev ? min(max(*split_dev, pages_per_split_arg), kMaxSplitPages) : pages_per_split_arg;
-  for (int i = threadIdx.x; i <= kMaxSplitPages; i += blockDim.x) hist[i] = 0;
   for (int i = threadIdx.x; i < kPrefillClasses; i += blockDim.x) phist[i] = 0;
+  if (threadIdx.x == 0) s_pages = 0;
   __syncthreads();
-  // pass 1: sizes of the items.  A decode row of P pages gets ns = ceil(P / C) splits of P / ns pages
-  // (the first P % ns of them one page more), so every split of a long row holds C/2 .. C pages.  A
-  // prefill row gets one item per q_tile new tokens, sized by prefill_class.
+  // pass 1: the step's decode pages T, and the prefill items per size class
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
     const int s = base + threadIdx.x;
     const int nn = s < num_seqs ? qo_indptr[s + 1] - qo_indptr[s] : 0;
     if (nn == 1) {
-      const int pages = kv_indptr[s + 1] - kv_indptr[s];
-      const int ns = (pages + pages_per_split - 1) / pages_per_split;
-      const int q = pages / ns, rem = pages - q * ns;
-      atomicAdd(&hist[q], ns - rem);
-      if (rem) atomicAdd(&hist[q + 1], rem);
+      atomicAdd(&s_pages, (unsigned long long)max(kv_indptr[s + 1] - kv_indptr[s], 0));
     } else if (nn > 1) {
       const int cached = seq_lens[s] - nn;
       for (int t0 = 0; t0 < nn; t0 += q_tile) atomicAdd(&phist[prefill_class(cached, t0, nn, q_tile)], 1);
     }
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {  // largest items first: the short ones fill the tail of the launch
-    int run = 0;
-    for (int sz = kMaxSplitPages; sz >= 1; --sz) {
-      offs[sz] = run;
-      run += hist[sz];
-    }
-  }
+  __syncthreads();  // every count is in before the scan reads them
   {  // prefill classes in descending order: thread t scans class kPrefillClasses - 1 - t
     const int cls = kPrefillClasses - 1 - (int)threadIdx.x;
     int total;
@@ -102,48 +100,88 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
     phist[cls] = off;  // from here on: the next free position of the class
   }
   __syncthreads();
-  // pass 2: emit.  A decode item carries its row's canonical partial slot (row-major order), which is
-  // where the merge looks for it whatever its position in the launch.
-  int base_d = 0, base_m = 0;
+  const int64_t total = (int64_t)s_pages;
+  const int nb = total ? (int)((total + pages_per_split - 1) / pages_per_split) : 0;
+
+  // Decode rows' pages, in sequence order, form one stream of T pages cut into nb bins of floor / ceil
+  // (T / nb) pages; a row's segment in a bin is the part of the row that bin holds.  Passes 2 and 3 walk
+  // the rows with the same scans: pass 2 counts segments, partial slots and merges to check the
+  // capacities, pass 3 writes them.
+  int n_seg = 0, n_slot = 0, n_merge = 0;
+  bool fits = false;
+  for (int pass = 2; pass <= 3; ++pass) {
+    int64_t base_p = 0;
+    int base_g = 0, base_sl = 0, base_m = 0;
+    for (int base = 0; base < num_seqs; base += kPlanThreads) {
+      const int s = base + threadIdx.x;
+      const int nn = s < num_seqs ? qo_indptr[s + 1] - qo_indptr[s] : 0;
+      const int pages = nn == 1 ? max(kv_indptr[s + 1] - kv_indptr[s], 0) : 0;
+      int tp;
+      const int64_t off = base_p + wg_exclusive_scan(pages, sums, &tp);
+      int first = 0, nseg = 0;
+      if (pages > 0) {
+        first = bin_of(off, total, nb);
+        nseg = bin_of(off + pages - 1, total, nb) - first + 1;
+      }
+      const bool cut = nseg > 1;
+      int tg, tsl, tm;
+      const int g0 = base_g + wg_exclusive_scan(nseg, sums, &tg);
+      const int sl0 = base_sl + wg_exclusive_scan(cut ? nseg : 0, sums, &tsl);
+      const int m0 = base_m + wg_exclusive_scan(cut ? 1 : 0, sums, &tm);
+      if (pass == 3 && fits && nseg > 0) {
+        // segment records: {first page in kv_indices, pages, first page within the row, row length},
+        // {q row, partial slot (-1: the row's only segment writes the output), sequence, 0}
+        int4* segs = decode_work + 1 + nb;
+        const int kv0 = kv_indptr[s], len = seq_lens[s], qrow = qo_indptr[s];
+        for (int j = 0; j < nseg; ++j) {
+          const int b = first + j;
+          const int64_t bs0 = bin_start(b, total, nb), bs1 = bin_start(b + 1, total, nb);
+          const int lo = (int)(max(off, bs0) - off), hi = (int)(min(off + pages, bs1) - off);
+          const int g = g0 + j;
+          segs[2 * g] = make_int4(kv0 + lo, hi - lo, lo, len);
+          segs[2 * g + 1] = make_int4(qrow, cut ? sl0 + j : -1, s, 0);
+          if (j > 0 || bs0 == off) {  // bin b starts in this row
+            decode_work[1 + b].x = g;
+            decode_work[1 + b].z = 1 + nb;  // the record index of segment 0
+          }
+          if (bs1 <= off + pages) decode_work[1 + b].y = g + 1;   // and ends in it
+        }
+        if (cut) merge_work[m0] = make_int4(s, sl0, nseg, 0);
+      }
+      base_p += tp;
+      base_g += tg;
+      base_sl += tsl;
+      base_m += tm;
+    }
+    if (pass == 2) {
+      n_seg = base_g;
+      n_slot = base_sl;
+      n_merge = base_m;
+      // a step larger than the capacities gets no decode work at all, so the decode and merge kernels
+      // never index past a workspace sized for cap_decode partial slots
+      fits = nb > 0 && 1 + (int64_t)nb + 2 * (int64_t)n_seg <= cap_decode && n_merge <= cap_merge &&
+             n_slot <= cap_decode;
+    }
+  }
+  if (threadIdx.x == 0 && cap_decode > 0)
+    decode_work[0] = fits ? make_int4(nb, n_seg, n_slot, 0) : make_int4(0, 0, 0, 0);
+
+  // prefill items, longest first
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
     const int s = base + threadIdx.x;
-    int nd = 0, nm = 0, pages = 0;
-    bool pf = false;
-    if (s < num_seqs) {
-      const int nn = qo_indptr[s + 1] - qo_indptr[s];
-      pages = kv_indptr[s + 1] - kv_indptr[s];
-      if (nn == 1) {
-        nd = (pages + pages_per_split - 1) / pages_per_split;
-        nm = nd > 1 ? 1 : 0;
-      } else {
-        pf = nn > 1;
+    if (s >= num_seqs) continue;
+    const int qs = qo_indptr[s], nn = qo_indptr[s + 1] - qs;
+    if (nn <= 1) continue;
+    // {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: what the prefill kernel reads per item
+    const int cached = seq_lens[s] - nn, kv0 = kv_indptr[s];
+    for (int t0 = 0; t0 < nn; t0 += q_tile) {
+      const int pos = atomicAdd(&phist[prefill_class(cached, t0, nn, q_tile)], 1);
+      const int kv_end = cached + min(t0 + q_tile, nn);
+      if (pos < cap_prefill) {
+        prefill_work[2 * pos] = make_int4(s, t0, qs, nn);
+        prefill_work[2 * pos + 1] = make_int4(cached, kv0, kv_end, (kv_end + kPrefillKeyTile - 1) / kPrefillKeyTile);
       }
     }
-    int td, tm;
-    const int od = base_d + wg_exclusive_scan(nd, sums, &td);
-    const int om = base_m + wg_exclusive_scan(nm, sums, &tm);
-    // An item is emitted only when its position and its partial slot are inside the capacities, and a
-    // merge item only when every slot of its row is: a step larger than the caller sized for loses
-    // those rows' items instead of writing or reading partials past the workspace.
-    for (int j = 0; j < nd; ++j) {
-      const int sz = (int)(((int64_t)(j + 1) * pages) / nd - ((int64_t)j * pages) / nd);
-      const int pos = atomicAdd(&offs[sz], 1);
-      if (pos < cap_decode && od + j < cap_decode) decode_work[pos] = make_int4(s, j, nd, od + j);
-    }
-    if (nm && om < cap_merge && od + nd <= cap_decode) merge_work[om] = make_int4(s, od, nd, 0);
-    if (pf) {  // {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: what the prefill kernel reads per item
-      const int qs = qo_indptr[s], nn = qo_indptr[s + 1] - qs, cached = seq_lens[s] - nn, kv0 = kv_indptr[s];
-      for (int t0 = 0; t0 < nn; t0 += q_tile) {
-        const int pos = atomicAdd(&phist[prefill_class(cached, t0, nn, q_tile)], 1);
-        const int kv_end = cached + min(t0 + q_tile, nn);
-        if (pos < cap_prefill) {
-          prefill_work[2 * pos] = make_int4(s, t0, qs, nn);
-          prefill_work[2 * pos + 1] = make_int4(cached, kv0, kv_end, (kv_end + kPrefillKeyTile - 1) / kPrefillKeyTile);
-        }
-      }
-    }
-    base_d += td;
-    base_m += tm;
   }
 }
 

@@ -16,7 +16,7 @@ LIB_PATH = Path(os.environ.get("MLLM_HIP_LIB", Path(__file__).resolve().parent /
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

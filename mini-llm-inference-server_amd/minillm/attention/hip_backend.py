@@ -28,18 +28,29 @@ import torch
 
 from .. import _native
 from .base import AttentionBackend
+from .metadata import decode_plan_size
 
-# A decode split is sized so that all splits of a step make about one round of resident wavefronts
-# (256 CUs x 12 decode wavefronts), clamped to [8, 128] pages; on the 256-row decode workload this
-# gives ~90-page splits, the measured optimum (96 pages: 360 us vs 370 us at 64 and 418 us at 32).
-TARGET_DECODE_WAVES = 256 * 12
+def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool) -> tuple[int, int]:
+    """(resident wavefronts of the decode kernel on the chip, wavefronts one bin takes): 256 CUs x 4 SIMDs
+    x 3 per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two KV
+    heads when they pair up (decode_kernel_name), else one per KV head."""
+    if not kv_fp8:
+        return 256 * 4 * 3, num_kv_heads
+    if decode_kernel_name(True, num_heads, num_kv_heads) == "decode_pair_kernel":
+        return 256 * 4 * 2, num_kv_heads // 2
+    return 256 * 4 * 2, num_kv_heads
 
 
-def pages_per_split(decode_pages: int, num_kv_heads: int) -> int:
+def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None = None, kv_fp8: bool = False) -> int:
+    """Pages per decode bin: the step's bins make one round of the kernel's resident wavefronts, clamped to
+    [8, 128] pages (~89 pages on the 256-row decode workload with a bf16 pool, ~67 with an fp8 one).  More
+    rounds of smaller bins measured slower (60 and 45 pages on bf16 decode_256: +10% and +7%), and so do
+    bins that leave resident wavefronts idle (fp8 pool at 89 pages: +10%)."""
     forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
     if forced:
         return max(1, min(128, int(forced)))
-    return max(8, min(128, math.ceil(decode_pages * num_kv_heads / TARGET_DECODE_WAVES)))
+    slots, per_bin = decode_waves(num_heads or 4 * num_kv_heads, num_kv_heads, kv_fp8)
+    return max(8, min(128, math.ceil(decode_pages * per_bin / slots)))
 
 
 @dataclass
@@ -48,7 +59,7 @@ class StepPlan:
 
     pages_per_split: int
     q_tile: int
-    num_decode: int
+    num_decode: int  # int4 records of the decode plan (its capacity)
     num_merge: int
     num_prefill: int
     decode_work: torch.Tensor
@@ -87,13 +98,17 @@ class HipBackend(AttentionBackend):
     # The model hands q and k to `forward_rotary` before RoPE when this is set (LlamaAttention checks it),
     # so the rotation runs in the KV-append launch; False gives the reference call sequence.
     fuse_rotary = True
-    # A step with decode rows and multi-token rows runs the prefill launch on a second stream beside the
-    # decode launch (HBM-bound and MFMA-bound work overlap); their outputs are disjoint rows of `out`.
-    overlap_mixed = True
+    # When set, a step with decode rows and multi-token rows runs the prefill launch on a second stream
+    # beside the decode launch; their outputs are disjoint rows of `out`.  Off by default: the decode
+    # launch is one round of equal bins that keeps every SIMD busy until it ends, so the prefill's
+    # workgroups (a whole CU each) find no room beside it.  On mixed_128, one box: 410.8 us one after the
+    # other, 412.8 us overlapped with decode enqueued first, 413.5 us with prefill first.
+    overlap_mixed = False
 
     def __init__(self) -> None:
         self._lib = _native.lib()
         self._planned = None  # the AttentionMetadata the plan was last built for
+        self._planned_fp8 = False  # and the pool type it was built for
         self._plan: StepPlan | None = None
         self._workspace: torch.Tensor | None = None
         self._side: dict = {}  # device -> the stream mixed steps run their prefill launch on
@@ -193,18 +208,17 @@ class HipBackend(AttentionBackend):
         capture records that build, so every replay re-plans from the staged metadata)."""
         self._planned = None
 
-    def plan(self, meta, num_heads: int, num_kv_heads: int, head_dim: int, device) -> StepPlan:
-        """The step's work plan, built on the GPU once per `meta` object and reused after."""
-        if self._planned is not meta:
-            self._make_plan(meta, num_heads, num_kv_heads, head_dim, device, _native.stream_ptr(device))
+    def plan(self, meta, num_heads: int, num_kv_heads: int, head_dim: int, device, kv_fp8: bool = False) -> StepPlan:
+        """The step's work plan, built on the GPU once per `meta` object (and pool type) and reused after."""
+        if self._planned is not meta or self._planned_fp8 != kv_fp8:
+            self._make_plan(meta, num_heads, num_kv_heads, head_dim, device, _native.stream_ptr(device), kv_fp8)
         return self._plan
 
     def attend(self, q, k_cache, v_cache, meta, out, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
         """Attention of every new token over its row's context in the pool, written into `out`."""
-        plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device)
+        plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device, is_fp8(k_cache))
         if plan.num_decode and plan.num_prefill and self.overlap_mixed and not torch.cuda.is_current_stream_capturing():
-            # decode is enqueued first (its small items spread over the chip first; the prefill's
-            # workgroups fill in as they free up): measured faster than the prefill-first order
+            # decode is enqueued first; the prefill's workgroups take CUs as the decode's free up
             cur = torch.cuda.current_stream(q.device)
             side = self._side.get(q.device)
             if side is None:
@@ -263,20 +277,20 @@ class HipBackend(AttentionBackend):
         else:
             self._lib.call("mllm_paged_prefill", *args, *tail)
 
-    def _make_plan(self, meta, h: int, hkv: int, dh: int, dev, stream: int) -> None:
+    def _make_plan(self, meta, h: int, hkv: int, dh: int, dev, stream: int, kv_fp8: bool = False) -> None:
         news, lens, bs = meta.num_new, meta.seq_lens, meta.block_size
         pages = [-(-length // bs) for length in lens]
         decode_pages = sum(p for p, nn in zip(pages, news) if nn == 1)
         # a graph-captured step (StaticDecodeMetadata) stages its split size on the device; the
         # capacities then cover the smallest split it may stage
         split_dev = getattr(meta, "split_dev", None)
-        c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv)
+        c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv, h, kv_fp8)
         g = h // hkv
         q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
-        n_dec = sum(-(-p // c) for p, nn in zip(pages, news) if nn == 1)
-        if split_dev is not None:  # a captured step sized for fewer items than its worst case
-            n_dec = min(n_dec, meta.decode_items_cap)
-        n_merge = sum(1 for p, nn in zip(pages, news) if nn == 1 and p > c)
+        decode_rows = sum(1 for nn in news if nn == 1)
+        n_dec, n_merge = decode_plan_size(decode_pages, decode_rows, c)
+        if split_dev is not None:  # a captured step sized for fewer records than its worst case
+            n_dec = min(n_dec, meta.decode_records_cap)
         n_pf = sum(-(-nn // q_tile) for nn in news if nn > 1)
         buf = torch.full((4 * n_dec + 4 * n_merge + 8 * n_pf,), -1, dtype=torch.int32, device=dev)
         dec, mrg, pf = buf[:4 * n_dec], buf[4 * n_dec:4 * (n_dec + n_merge)], buf[4 * (n_dec + n_merge):]
@@ -290,7 +304,7 @@ class HipBackend(AttentionBackend):
                            _ptr(pf), n_pf, stream)
         ws = self._lib.workspace_bytes(n_dec, h, dh) if n_merge else 0
         self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws)
-        self._planned = meta
+        self._planned, self._planned_fp8 = meta, kv_fp8
 
     def _workspace_for(self, nbytes: int, dev) -> torch.Tensor | None:
         if nbytes == 0:

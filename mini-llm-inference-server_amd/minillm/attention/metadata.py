@@ -245,6 +245,16 @@ def pack_steps(seqs: list[SeqStep], out: np.ndarray) -> np.ndarray:
     return out[:3 * n_seq + 1 + n_ids]
 
 
+def decode_plan_size(decode_pages: int, decode_rows: int, pages_per_split: int) -> tuple[int, int]:
+    """int4 records and merge items that hold a step's decode plan (mllm_plan): a header, one record per bin
+    and two per segment, with bins = ceil(pages / pages_per_split).  A row is cut only where a bin boundary
+    falls inside it, so segments <= bins + rows - 1 and cut rows <= min(rows, bins - 1)."""
+    if decode_rows <= 0 or decode_pages <= 0:
+        return 0, 0
+    bins = -(-decode_pages // pages_per_split)
+    return 1 + bins + 2 * (bins + decode_rows - 1), min(decode_rows, bins - 1)
+
+
 class StaticDecodeMetadata:
     """Metadata of a decode step of exactly `num_rows` rows (one new token each) in fixed device buffers,
     for HIP graph capture: the arenas, the upload buffer and its pinned host twin never move, and the
@@ -260,14 +270,15 @@ class StaticDecodeMetadata:
     SPLIT_MIN = 8  # the smallest split the host heuristic picks
 
     def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int,
-                 decode_items: int | None = None) -> None:
-        """`decode_items` caps the plan's split-KV items (default: every row at `max_blocks` blocks in
-        splits of SPLIT_MIN pages); a step whose items at its staged split size exceed it must not be
-        staged (see items())."""
+                 decode_records: int | None = None) -> None:
+        """`decode_records` caps the plan's decode records (default: every row at `max_blocks` blocks in
+        splits of SPLIT_MIN pages); a step whose plan at its staged split size needs more must not be
+        staged (see records())."""
         self.num_rows, self.tables, self.block_size = num_rows, tables, block_size
         self.max_blocks = tables.max_blocks
-        worst = num_rows * -(-self.max_blocks // self.SPLIT_MIN)
-        self.decode_items = worst if decode_items is None else max(num_rows, min(worst, int(decode_items)))
+        worst, _ = decode_plan_size(num_rows * self.max_blocks, num_rows, self.SPLIT_MIN)
+        least, _ = decode_plan_size(num_rows, num_rows, self.SPLIT_MIN)  # every row one page
+        self.decode_records = worst if decode_records is None else max(least, min(worst, int(decode_records)))
         dev = tables.device
         # num_cached | num_new | rows | num_blocks | split size | table updates (at most every entry of B rows)
         self._upd = 4 * num_rows + 1
@@ -282,18 +293,18 @@ class StaticDecodeMetadata:
                                               num_rows * self.max_blocks, dev)
         self.meta.split_dev = self.packed[4 * num_rows:4 * num_rows + 1]
         self.meta.split_min = self.SPLIT_MIN
-        self.meta.decode_items_cap = self.decode_items
+        self.meta.decode_records_cap = self.decode_records
 
     def split_size(self, pages_per_split: int) -> int:
         """The split size a staged step runs with (what mllm_plan_dev clamps it to)."""
         return max(self.SPLIT_MIN, min(128, int(pages_per_split)))
 
-    def items(self, seqs: list[SeqStep], pages_per_split: int) -> int:
-        """Split-KV items of the step at its staged split size, padding rows included (one page each)."""
-        c = self.split_size(pages_per_split)
+    def records(self, seqs: list[SeqStep], pages_per_split: int) -> int:
+        """Decode plan records the step needs at its staged split size, padding rows included (one page
+        each)."""
         bs = self.block_size
-        pages = [-(-(s.num_cached + 1) // bs) for s in seqs]
-        return sum(-(-p // c) for p in pages) + (self.num_rows - len(seqs))
+        pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs) + (self.num_rows - len(seqs))
+        return decode_plan_size(pages, self.num_rows, self.split_size(pages_per_split))[0]
 
     def load(self, keys, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
         """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host packing,

@@ -12,13 +12,14 @@ A step then costs the host one packed upload of (num_cached, num_new, block tabl
 one graph launch and the read of B token ids.
 
 The graph is captured with fixed sizes.  A row may hold up to ceil(max_model_len / block_size) blocks;
-the plan's split-KV capacity of a B-row bucket is the smaller of B rows at that length in the smallest
-splits and the whole pool in the smallest splits plus one item per row (without prefix sharing, a step's
-pages never exceed the pool).  Each replay stages the split size an eager step of the same rows would
+the decode plan's capacity of a B-row bucket covers the fewer pages of B rows at that length and the
+whole pool plus one page per row (without prefix sharing, a step's pages never exceed the pool), in
+bins of the smallest split size.  Each replay stages the split size an eager step of the same rows would
 use (mllm_plan_dev reads it on the device), so a replayed step runs the same decode work as the eager
-one; a step whose items at that size exceed the bucket's capacity (rows sharing prefix pages can) is
-not replayed but run eagerly (`fits`).  The plan slots a step leaves unused stay -1, which every kernel
-skips.  Rows past the step's own are padding (see StaticDecodeMetadata).  All buckets share one decode
+one; a step whose plan at that size exceeds the bucket's capacity (rows sharing prefix pages can) is
+not replayed but run eagerly (`fits`).  Every replay fills the plan buffers with -1 before planning,
+and the decode and merge launches cover the capacity: workgroups past the step's own bins and merges
+exit at once.  Rows past the step's own are padding (see StaticDecodeMetadata).  All buckets share one decode
 workspace, sized for the largest: replays run one at a time on the engine's stream.
 Only pure decode steps run as graphs; prefill and mixed steps run eagerly.
 """
@@ -28,7 +29,7 @@ from __future__ import annotations
 import torch
 
 from ..attention.hip_backend import pages_per_split
-from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata
+from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata, decode_plan_size
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
 
@@ -71,21 +72,21 @@ class DecodeGraphs:
         return next(b for b in self.buckets if b >= num_rows)
 
     def capacity(self, bucket: int) -> int:
-        """Split-KV items the bucket's plan holds."""
-        c = StaticDecodeMetadata.SPLIT_MIN
-        worst = bucket * -(-self.tables.max_blocks // c)
-        return min(worst, -(-self.cache.num_blocks // c) + bucket)
+        """Decode plan records the bucket's plan holds: its rows at max_model_len, or the whole pool plus one
+        page per row, whichever is fewer pages, in bins of SPLIT_MIN pages."""
+        pages = min(bucket * self.tables.max_blocks, self.cache.num_blocks + bucket)
+        return decode_plan_size(pages, bucket, StaticDecodeMetadata.SPLIT_MIN)[0]
 
     def fits(self, seqs: list[SeqStep]) -> bool:
-        """Whether the decode step `seqs` can replay a graph: a bucket holds its rows, and its split-KV
-        items at the split size it would stage fit that bucket's plan."""
+        """Whether the decode step `seqs` can replay a graph: a bucket holds its rows, and its decode plan at
+        the split size it would stage fits that bucket's plan."""
         if not self.supports(len(seqs)):
             return False
         b = self.bucket(len(seqs))
-        pages = [-(-(s.num_cached + 1) // self.block_size) for s in seqs]
-        c = max(StaticDecodeMetadata.SPLIT_MIN, min(128, pages_per_split(sum(pages), self.num_kv_heads)))
-        items = sum(-(-p // c) for p in pages) + (b - len(seqs))
-        if items <= self.capacity(b):
+        pages = sum(-(-(s.num_cached + 1) // self.block_size) for s in seqs)
+        c = max(StaticDecodeMetadata.SPLIT_MIN, min(128, self._split(pages)))
+        records, _ = decode_plan_size(pages + (b - len(seqs)), b, c)  # padding rows hold one page each
+        if records <= self.capacity(b):
             return True
         self.eager_fallbacks += 1
         return False
@@ -110,10 +111,14 @@ class DecodeGraphs:
 
     # ------------------------------------------------------------------ internals
 
+    def _split(self, pages: int) -> int:
+        """The split size an eager step over `pages` decode pages uses with this pool."""
+        return pages_per_split(pages, self.num_kv_heads, self.num_heads, self.cache.quantized)
+
     def _stage(self, c: _Captured, keys, seqs: list[SeqStep], token_ids: list[int]) -> None:
         bs = self.block_size
         pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs)
-        c.static.load(keys, seqs, pages_per_split(pages, self.num_kv_heads))  # the eager step's split size
+        c.static.load(keys, seqs, self._split(pages))  # the eager step's split size
         # the previous step's copy out of the same pinned memory may still be queued behind its replay
         # (a sampler need not wait for the GPU): let it run before the host rewrites the ids
         c.ids_uploaded.synchronize()
@@ -133,7 +138,7 @@ class DecodeGraphs:
 
     @torch.inference_mode()
     def _capture(self, bucket: int) -> _Captured:
-        static = StaticDecodeMetadata(bucket, self.tables, self.block_size, decode_items=self.capacity(bucket))
+        static = StaticDecodeMetadata(bucket, self.tables, self.block_size, decode_records=self.capacity(bucket))
         c = _Captured(static, torch.zeros((1, bucket), dtype=torch.long, device=self.device),
                       torch.zeros(bucket, dtype=torch.long, pin_memory=True))
         self._stage(c, [], [], [])  # every row padding: a valid step that writes nothing to the pool

@@ -14,6 +14,7 @@ from pathlib import Path
 import pytest
 import torch
 
+import decode_plan
 from harness import ATOL, RTOL, bits, hip_step, oracle_step
 from oracle.metadata import OracleSeq, build_metadata
 
@@ -349,12 +350,13 @@ def test_plan_is_reused_per_metadata(hip):
 
 
 def test_plan_contents(hip):
-    # the GPU plan against the rules it implements, on rows of many lengths: a decode row of P pages gets
-    # ns = ceil(P / C) balanced splits with canonical partial slots, launched largest split first; a
-    # prefill row gets one item per q_tile new tokens, launched in decreasing number of 64-key tiles its
-    # causal context spans
+    # the GPU plan against the rules it implements, on rows of many lengths.  Decode rows' pages, rows in
+    # sequence order, form one stream of T pages cut into nb = ceil(T / C) bins of floor / ceil(T / nb)
+    # pages; a row's part in a bin is a segment, rows cut into several segments get consecutive partial
+    # slots and one merge item.  A prefill row gets one item per q_tile new tokens, launched in decreasing
+    # number of 64-key tiles its causal context spans
     from minillm.attention.hip_backend import HipBackend
-    from minillm.attention.metadata import AttentionMetadata, SeqStep
+    from minillm.attention.metadata import AttentionMetadata, SeqStep, decode_plan_size
 
     rng = random.Random(7)
     steps = [(rng.randrange(0, 5000), rng.choice([1, 1, 2, 40, 200])) for _ in range(300)]
@@ -369,36 +371,33 @@ def test_plan_contents(hip):
     p = backend._plan
     c = p.pages_per_split
     dec = p.decode_work.view(-1, 4).cpu().tolist()
-    exp_dec, exp_merge, exp_pf = [], [], []
-    for s, (cached, n) in enumerate(steps):
-        pages = -(-(cached + n) // 16)
-        if n == 1:
-            ns = -(-pages // c)
-            first = len(exp_dec)
-            exp_dec += [[s, j, ns, first + j] for j in range(ns)]
-            if ns > 1:
-                exp_merge.append([s, first, ns, 0])
-        else:
-            nt = -(-n // p.q_tile)
-            exp_pf += [[s, (nt - 1 - j) * p.q_tile] for j in range(nt)]
-    assert sorted(dec) == sorted(exp_dec)
-
-    def size(item):
-        s, j, ns, _ = item
-        pages = -(-sum(steps[s]) // 16)
-        return (j + 1) * pages // ns - j * pages // ns
-
-    sizes = [size(it) for it in dec]
-    assert sizes == sorted(sizes, reverse=True) and max(sizes) <= c
-    assert p.merge_work.view(-1, 4).cpu().tolist() == exp_merge
-    recs = p.prefill_work.view(-1, 8).cpu().tolist()
-    assert sorted(r[:2] for r in recs) == sorted(exp_pf)
     starts = [0]
     for _, n in steps:
         starts.append(starts[-1] + n)
     kv_starts = [0]
-    for c, n in steps:
-        kv_starts.append(kv_starts[-1] + -(-(c + n) // 16))
+    for cc, n in steps:
+        kv_starts.append(kv_starts[-1] + -(-(cc + n) // 16))
+    rows = [(s, -(-(cc + n) // 16), kv_starts[s], starts[s], cc + n) for s, (cc, n) in enumerate(steps) if n == 1]
+    bins, exp_segs, exp_merge, slot = decode_plan.restate(rows, c)
+    nb, total = len(bins), sum(r[1] for r in rows)
+    assert dec[0] == [nb, len(exp_segs), slot, 0]
+    assert [r[:3] for r in dec[1:1 + nb]] == [b + [1 + nb] for b in bins]
+    got_segs = dec[1 + nb:1 + nb + 2 * len(exp_segs)]
+    assert [(got_segs[2 * i], got_segs[2 * i + 1]) for i in range(len(exp_segs))] == exp_segs
+    sizes = [sum(exp_segs[g][0][1] for g in range(b0, b1)) for b0, b1 in bins]
+    assert max(sizes) - min(sizes) <= 1 and max(sizes) <= c
+    assert all(seg[0][1] <= 128 for seg in exp_segs)
+    n_rec, n_merge = decode_plan_size(total, len(rows), c)
+    assert 1 + nb + 2 * len(exp_segs) <= n_rec == p.num_decode and len(exp_merge) <= n_merge == p.num_merge
+    mw = p.merge_work.view(-1, 4).cpu().tolist()
+    assert mw[:len(exp_merge)] == exp_merge and all(r[0] == -1 for r in mw[len(exp_merge):])
+    exp_pf = []
+    for s, (cc, n) in enumerate(steps):
+        if n > 1:
+            nt = -(-n // p.q_tile)
+            exp_pf += [[s, (nt - 1 - j) * p.q_tile] for j in range(nt)]
+    recs = p.prefill_work.view(-1, 8).cpu().tolist()
+    assert sorted(r[:2] for r in recs) == sorted(exp_pf)
     for s, t0, qs, nn, cached, kv0, kv_end, ntiles in recs:
         c, n = steps[s]
         assert (qs, nn, cached, kv0) == (starts[s], n, c, kv_starts[s])

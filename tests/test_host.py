@@ -98,7 +98,9 @@ def test_split_size_heuristic(monkeypatch):
     assert hip_backend.pages_per_split(10, 8) == 8
     assert hip_backend.pages_per_split(10 ** 7, 8) == 128
     c = hip_backend.pages_per_split(34000, 8)
-    assert 80 <= c <= 100
+    assert 80 <= c <= 100  # one round of the 16-bit kernel's 3,072 wavefronts, one per KV head per bin
+    assert hip_backend.pages_per_split(34000, 8, 32, kv_fp8=True) == 67  # fp8 pair kernel: 2,048, one per 2 heads
+    assert hip_backend.pages_per_split(34000, 7, 28, kv_fp8=True) == 117  # fp8 one-head kernel: 2,048, one per head
     monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", "5")
     assert hip_backend.pages_per_split(34000, 8) == 5
 
@@ -167,3 +169,37 @@ def test_resident_tables_send_only_new_block_ids():
     t.sync(["d"], [SeqStep(0, 1, [1])])
     with pytest.raises(ValueError, match="more than 3 requests"):
         t.sync(["e"], [SeqStep(0, 1, [1])])
+
+
+def test_decode_plan_size_bounds_every_plan():
+    # decode_plan_size (what the backend and the decode graphs allocate) holds the decode plan, restated in
+    # tests/decode_plan.py, and the grid the decode launch derives from it ((records - 1) // 3 bins) covers
+    # the plan's bins: one row, many one-page rows, rows shorter and longer than a bin, fewer pages than one
+    # bin, and random steps; every page of every row lies in exactly one segment, in order
+    import random
+
+    import decode_plan
+    from minillm.attention.metadata import decode_plan_size
+
+    rng = random.Random(11)
+    cases = [[1], [1] * 300, [5000], [3, 3, 3], [89] * 384, [7], [128, 1, 128]]
+    cases += [[rng.randrange(1, 600) for _ in range(rng.randrange(1, 400))] for _ in range(60)]
+    for pages in cases:
+        total = sum(pages)
+        for c in sorted({8, 89, 128, max(8, min(128, -(-total * 8 // 3072)))}):
+            rows = [(i, pg, 1000 * i, i, 16 * pg - 3) for i, pg in enumerate(pages)]
+            bins, segs, merges, slots = decode_plan.restate(rows, c)
+            n_rec, n_merge = decode_plan_size(total, len(pages), c)
+            assert 1 + len(bins) + 2 * len(segs) <= n_rec and len(merges) <= n_merge
+            assert (n_rec - 1) // 3 >= len(bins) == -(-total // c)
+            assert slots == sum(m[2] for m in merges) <= len(segs)
+            assert all(0 < r0[1] <= c for r0, _ in segs)  # at most 128 page ids per wavefront
+            sizes = [sum(segs[g][0][1] for g in range(b0, b1)) for b0, b1 in bins]
+            assert max(sizes) - min(sizes) <= 1
+            covered = {}
+            for r0, r1 in segs:
+                seq = r1[2]
+                assert r0[2] == covered.get(seq, 0) and r0[0] == 1000 * seq + r0[2]
+                covered[seq] = r0[2] + r0[1]
+            assert covered == {i: pg for i, pg in enumerate(pages)}
+    assert decode_plan_size(0, 0, 8) == (0, 0)
