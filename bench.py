@@ -392,8 +392,9 @@ def shared_step_costs(wl, backend, dev, reps: int = 10):
 def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
     """One layer's step on the GPU: KV append, decode + merge, prefill, launched one after another on
     the current stream; `warmup` untimed steps, then `steps` timed ones between two synchronisations,
-    with HIP events on that stream around every decode and prefill launch.  Mixed workloads also time
-    the backend's own step (prefill launch on a second stream beside decode + merge)."""
+    then the same `steps` again with HIP events on that stream around every decode and prefill launch
+    (the kernels' own durations; the events stay out of the timed steps).  Mixed workloads also time the
+    backend's own step (`attend`)."""
     import torch
 
     from minillm.attention.metadata import AttentionMetadata, SeqStep
@@ -432,11 +433,15 @@ def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     start.record()
-    for i in range(steps):
-        step(evs[i])
+    for _ in range(steps):  # the timed steps: no events between their launches
+        step()
     stop.record()
     torch.cuda.synchronize()
-    res = {"wall_ms": (time.perf_counter() - w0) * 1e3, "step_ms": start.elapsed_time(stop) / steps,
+    wall_ms = (time.perf_counter() - w0) * 1e3
+    for i in range(steps):  # the same steps again, with HIP events around each launch: the kernels' own time
+        step(evs[i])
+    torch.cuda.synchronize()
+    res = {"wall_ms": wall_ms, "step_ms": start.elapsed_time(stop) / steps,
            "dec_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0,
            "pf_ms": statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0,
            "plan": plan, "meta": meta, "tensors": (q, k, v, pool_k, pool_v)}
