@@ -406,6 +406,86 @@ def test_plan_contents(hip):
     assert spans == sorted(spans, reverse=True) and len(set(spans)) > 20
 
 
+def test_plan_and_attention_over_more_rows_than_one_plan_chunk(hip):
+    # the plan walks the rows 1,024 at a time (its scans carry a base from chunk to chunk): 2,500 rows of
+    # every kind, the plan's decode records against their restatement and the outputs against the oracle
+    from minillm.attention.hip_backend import HipBackend
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    rng = random.Random(31)
+    steps = [(rng.randrange(0, 60), rng.choice([1, 1, 1, 1, rng.randrange(2, 20)])) for _ in range(2500)]
+    nb = sum(-(-(c + n) // 16) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=nb, seed=31)
+    out, pk, pv, meta = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+    backend = HipBackend()
+    backend._make_plan(meta, 32, 8, 128, torch.device(DEV), torch.cuda.current_stream().cuda_stream)
+    p = backend._plan
+    starts, kv_starts = [0], [0]
+    for c, n in steps:
+        starts.append(starts[-1] + n)
+        kv_starts.append(kv_starts[-1] + -(-(c + n) // 16))
+    rows = [(s, -(-(c + n) // 16), kv_starts[s], starts[s], c + n) for s, (c, n) in enumerate(steps) if n == 1]
+    bins, segs, merges, slot = decode_plan.restate(rows, p.pages_per_split)
+    dec = p.decode_work.view(-1, 4).cpu().tolist()
+    assert dec[0] == [len(bins), len(segs), slot, 0]
+    got = dec[1 + len(bins):1 + len(bins) + 2 * len(segs)]
+    assert [(got[2 * i], got[2 * i + 1]) for i in range(len(segs))] == segs
+    assert p.merge_work.view(-1, 4).cpu().tolist()[:len(merges)] == merges
+
+
+@pytest.mark.parametrize("pages_per_split", [8, 13])
+def test_decode_rows_with_pages_past_their_last_token(hip, pages_per_split):
+    # a caller's page lists may run past a row's last token (pages held ahead).  The plan counts those
+    # pages, so a bin boundary can leave a segment of such pages only, with no tile to stream: the wave
+    # must still load the next segment's first tile itself.  Decode rows with 0-5 extra pages each,
+    # through the C ABI, against the oracle on the same rows without them
+    from minillm import _native
+    from minillm.attention.hip_backend import HipBackend, _ptr
+    from minillm.attention.metadata import AttentionMetadata, SeqStep, decode_plan_size
+
+    rng = random.Random(21)
+    steps = [(rng.randrange(0, 300), 1) for _ in range(40)]
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=400, seed=21)
+    extra = [rng.randrange(0, 6) for _ in steps]
+    lists = [list(b) + [rng.randrange(wl.num_blocks) for _ in range(e)] for (_, _, b), e in zip(wl.seqs, extra)]
+    rows = [(i, len(lst), 0, i, c + 1) for i, ((c, _), lst) in enumerate(zip(steps, lists))]
+    _, segs, _, _ = decode_plan.restate(rows, pages_per_split)
+    assert any(r0[2] * 16 >= r0[3] for r0, _ in segs)  # some segment holds extra pages only
+
+    ref, rk, rv = oracle_step(wl, DEV)
+    meta = AttentionMetadata.build([SeqStep(c, n, list(b)) for c, n, b in wl.seqs], wl.block_size, DEV)
+    q, k, v = wl.q.to(DEV), wl.k.to(DEV), wl.v.to(DEV)
+    pk, pv = wl.pool_k.to(DEV), wl.pool_v.to(DEV)
+    HipBackend().append(k, v, pk, pv, meta)
+    kv_indptr = torch.tensor([0] + [sum(len(x) for x in lists[:i + 1]) for i in range(len(lists))],
+                             dtype=torch.int32, device=DEV)
+    kv_indices = torch.tensor([b for lst in lists for b in lst], dtype=torch.int32, device=DEV)
+    total = sum(len(x) for x in lists)
+    n_rec, n_merge = decode_plan_size(total, len(lists), pages_per_split)
+    dec = torch.full((4 * n_rec,), -1, dtype=torch.int32, device=DEV)
+    mrg = torch.full((4 * n_merge,), -1, dtype=torch.int32, device=DEV)
+    lib = _native.lib()
+    st = _native.stream_ptr(DEV)
+    lib.call("mllm_plan", meta.qo_indptr.data_ptr(), kv_indptr.data_ptr(), meta.seq_lens_i32.data_ptr(), len(lists),
+             pages_per_split, 64, dec.data_ptr(), n_rec, _ptr(mrg), n_merge, 0, 0, st)
+    ws = torch.empty(lib.workspace_bytes(n_rec, 32, 128), dtype=torch.uint8, device=DEV)
+    out = torch.full_like(q, float("nan"))
+    nb, bs, hkv, dh = pk.shape
+    lib.call("mllm_paged_decode", q.data_ptr(), q.stride(0), q.stride(1), pk.data_ptr(), pv.data_ptr(), nb, bs, 32,
+             hkv, dh, meta.qo_indptr.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+             meta.seq_lens_i32.data_ptr(), dec.data_ptr(), n_rec, _ptr(mrg), n_merge, pages_per_split, dh ** -0.5,
+             _native.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), st)
+    lib.call("mllm_merge_splits", _ptr(mrg), n_merge, n_rec, 32, dh, meta.qo_indptr.data_ptr(),
+             _native.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), st)
+    torch.cuda.synchronize()
+    assert dec[0].item() == -(-total // pages_per_split)  # the plan fit its capacity
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def test_prefill_item_without_visible_keys_writes_nothing(hip):
     # a plan record whose row has no visible key (kv_end 0: seq_lens below the new-token count, which the
     # metadata build never produces) makes the workgroup return before any load; out keeps its sentinel
