@@ -103,7 +103,7 @@ __device__ __forceinline__ int qk_dim0(int kk, int g) {
   return F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : 32 * kk + 8 * g;
 }
 
-// The next 16-token tile to load: its page within the split and its 16-token slice of that page (tiles
+// The next 16-token tile to load: its page within the segment and its 16-token slice of that page (tiles
 // are loaded in order, once each, so a counter replaces a division by the tiles per page).
 struct LoadCursor {
   int page = 0, sub = 0;
@@ -210,7 +210,18 @@ __device__ __forceinline__ void consume_tile(const u32x4 (&ka)[4], u32x4 (&va)[4
 struct SegRec {
   int4 r0, r1;
 };
-__device__ __forceinline__ SegRec seg_rec(const int4* segs, int g) { return SegRec{segs[2 * g], segs[2 * g + 1]}; }
+// The plan is read through the constant address space: it does not change during the launch, so its
+// uniform records become scalar loads, which the wave waits for with lgkmcnt apart from the vector
+// loads of K, V and q (read as global memory, a record would be a vector load, and waiting for it would
+// wait for every vector load issued before it).
+typedef const __attribute__((address_space(4))) int PlanInt;
+__device__ __forceinline__ int4 plan_rec(const int4* work, int i) {
+  const PlanInt* p = (const PlanInt*)(work + i);
+  return make_int4(p[0], p[1], p[2], p[3]);
+}
+__device__ __forceinline__ SegRec seg_rec(const int4* segs, int g) {
+  return SegRec{plan_rec(segs, 2 * g), plan_rec(segs, 2 * g + 1)};
+}
 
 // One wavefront per (bin, KV head) streams the bin's segments back to back, one 16-token tile ahead.
 // While a segment streams, the wavefront already holds the next segment's records (read one segment
@@ -230,8 +241,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   if (kvh >= a.Hkv) return;  // wave-uniform
   // the header and the bin's record load together (the record carries the segments' base): the
   // grid covers the plan's capacity, and workgroups past the step's nbins bins exit
-  const int nbins = a.work[0].x;
-  const int4 bw = a.work[1 + bin];
+  const int nbins = plan_rec(a.work, 0).x;
+  const int4 bw = plan_rec(a.work, 1 + bin);
   if (bin >= nbins) return;
   const int4* segs = a.work + bw.z;
   const int tpp = a.bs >> 4;
@@ -260,9 +271,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
     hi = lane + 64 < r0.y ? a.kv_indices[r0.x + 64 + lane] : 0;
   };
 
+  // The next segment's records, page ids and q are loaded whether or not there is a next segment (the
+  // last one's again, unused), so no loaded value meets a branch join: a join would make the wave wait
+  // there for every load in flight, the tile loaded ahead included.
+  const int glast = bw.y - 1;
   int gi = bw.x;
   SegRec cur = seg_rec(segs, gi);
-  SegRec nxt = gi + 1 < bw.y ? seg_rec(segs, gi + 1) : SegRec{};
+  SegRec nxt = seg_rec(segs, min(gi + 1, glast));
   int page_lo, page_hi;
   load_pages(cur.r0, page_lo, page_hi);
   u32x4 qf[4];
@@ -273,19 +288,17 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   at.advance(tpp);
 
   while (true) {
-    const bool has_next = gi + 1 < bw.y;
+    gi = __builtin_amdgcn_readfirstlane(gi);  // uniform: the records below are scalar loads
+    const bool has_next = gi < glast;
     const int tok0 = cur.r0.z * a.bs, len = cur.r0.w;
     // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
     // only such pages has none
     const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
-    int next_lo = 0, next_hi = 0;
-    u32x4 next_q[4] = {};
-    SegRec after = {};
-    if (has_next) {
-      load_pages(nxt.r0, next_lo, next_hi);
-      load_q(nxt.r1.x, next_q);
-      if (gi + 2 < bw.y) after = seg_rec(segs, gi + 2);
-    }
+    int next_lo, next_hi;
+    load_pages(nxt.r0, next_lo, next_hi);
+    u32x4 next_q[4];
+    load_q(nxt.r1.x, next_q);
+    const SegRec after = seg_rec(segs, min(gi + 2, glast));
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o[8];
 #pragma unroll
@@ -449,8 +462,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   const int bin = blockIdx.x / a.HG;
   const int kvh0 = 2 * (hg * W + (threadIdx.x >> 6));
   if (kvh0 >= a.Hkv) return;  // wave-uniform
-  const int nbins = a.work[0].x;
-  const int4 bw = a.work[1 + bin];
+  const int nbins = plan_rec(a.work, 0).x;
+  const int4 bw = plan_rec(a.work, 1 + bin);
   if (bin >= nbins) return;
   const int4* segs = a.work + bw.z;
   const int tpp = a.bs >> 4;
@@ -485,9 +498,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   const char* kbase = a.kc + kvh0 * kHeadDim;
   const char* vbase = a.vc + kvh0 * kHeadDim;
 
+  const int glast = bw.y - 1;  // next-segment loads as in decode_kernel: unconditional
   int gi = bw.x;
   SegRec cur = seg_rec(segs, gi);
-  SegRec nxt = gi + 1 < bw.y ? seg_rec(segs, gi + 1) : SegRec{};
+  SegRec nxt = seg_rec(segs, min(gi + 1, glast));
   int page_lo, page_hi;
   load_pages(cur.r0, page_lo, page_hi);
   u32x4 qa[4], qb[4];
@@ -502,19 +516,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   at.advance(tpp);
 
   while (true) {
-    const bool has_next = gi + 1 < bw.y;
+    gi = __builtin_amdgcn_readfirstlane(gi);
+    const bool has_next = gi < glast;
     const int tok0 = cur.r0.z * a.bs, len = cur.r0.w;
     // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
     // only such pages has none
     const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
-    int next_lo = 0, next_hi = 0;
-    u32x4 next_q[4] = {};
-    SegRec after = {};
-    if (has_next) {
-      load_pages(nxt.r0, next_lo, next_hi);
-      load_q(nxt.r1.x, next_q);
-      if (gi + 2 < bw.y) after = seg_rec(segs, gi + 2);
-    }
+    int next_lo, next_hi;
+    load_pages(nxt.r0, next_lo, next_hi);
+    u32x4 next_q[4];
+    load_q(nxt.r1.x, next_q);
+    const SegRec after = seg_rec(segs, min(gi + 2, glast));
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o[16];
 #pragma unroll
@@ -580,7 +592,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   }
 }
 
-// Log-sum-exp merge of a row's split partials: one workgroup per (row, head), one thread per dim.
+// Log-sum-exp merge of a cut row's partials (one per segment): one workgroup per (row, head), one thread
+// per dim.
 template <typename T>
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict__ merge, const float* __restrict__ part_o,
                                                          const float2* __restrict__ part_ml, int H,
@@ -591,8 +604,8 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
   if (seq < 0) return;
   const int head = blockIdx.y;
   const int d = threadIdx.x;
-  // one online pass over the splits, four at a time so that their loads are in flight together (a row
-  // has a few splits: one round trip instead of two per split); slots past n re-read split 0 of the
+  // one online pass over the partials, four at a time so that their loads are in flight together (a row
+  // has a few: one round trip instead of two per partial); slots past n re-read partial 0 of the
   // group and weigh it 2^-inf = 0
   constexpr int kGroup = 4;
   float m = -INFINITY, lsum = 0.f, acc = 0.f;
