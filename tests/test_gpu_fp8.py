@@ -168,6 +168,21 @@ def test_random_mixed_steps(hip, seed):
     _check(*fp8_step(wl, rng.uniform(0.02, 0.5), rng.uniform(0.02, 0.5)))
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_random_decode_heavy_steps(hip, seed):
+    # as the bf16 test of that name: 60-300 mostly-decode rows, block sizes 16 / 32 / 64, fp8 pools with
+    # random scales (the pair kernel's bins are sized for its own occupancy)
+    import random
+
+    rng = random.Random(4000 + seed)
+    bs = rng.choice([16, 32, 64])
+    steps = [(rng.randrange(0, rng.choice([16, 200, 1600])), rng.choice([1] * 9 + [rng.randrange(2, 90)]))
+             for _ in range(rng.randrange(60, 300))]
+    nb = sum(-(-(c + n) // bs) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, bs=bs, steps=steps, num_blocks=nb, seed=seed)
+    _check(*fp8_step(wl, rng.uniform(0.02, 0.5), rng.uniform(0.02, 0.5)))
+
+
 def _owned_slots(wl, include_new=True):
     used = torch.zeros(wl.num_blocks * wl.block_size, dtype=torch.bool)
     for c, n, blocks in wl.seqs:

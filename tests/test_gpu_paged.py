@@ -317,6 +317,23 @@ def test_random_mixed_steps(hip, seed):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_decode_heavy_steps(hip, seed):
+    # seeded steps of 60-300 rows, mostly decode, over contexts from one page to 100 pages and block sizes
+    # 16 / 32 / 64: the plan's equal bins cut rows at varied offsets (rows inside one bin, rows over
+    # several, bins of several rows); pools bit-exact, outputs within tolerance of the oracle
+    rng = random.Random(3000 + seed)
+    bs = rng.choice([16, 32, 64])
+    steps = [(rng.randrange(0, rng.choice([16, 200, 1600])), rng.choice([1] * 9 + [rng.randrange(2, 90)]))
+             for _ in range(rng.randrange(60, 300))]
+    nb = sum(-(-(c + n) // bs) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, bs=bs, steps=steps, seed=seed, num_blocks=nb)
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def test_llama_call_site_views(hip):
     # the model passes q[0].transpose(0, 1) of a [1, H, N, Dh] tensor: token stride Dh, head stride N*Dh
     from minillm.attention import get_backend
