@@ -272,8 +272,8 @@ class StaticDecodeMetadata:
     def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int,
                  decode_records: int | None = None) -> None:
         """`decode_records` caps the plan's decode records (default: every row at `max_blocks` blocks in
-        splits of SPLIT_MIN pages); a step whose plan at its staged split size needs more must not be
-        staged (see records())."""
+        bins of SPLIT_MIN pages); a step whose plan at its staged bin size needs more must not be staged
+        (DecodeGraphs.fits checks that on the host)."""
         self.num_rows, self.tables, self.block_size = num_rows, tables, block_size
         self.max_blocks = tables.max_blocks
         worst, _ = decode_plan_size(num_rows * self.max_blocks, num_rows, self.SPLIT_MIN)
@@ -298,13 +298,6 @@ class StaticDecodeMetadata:
     def split_size(self, pages_per_split: int) -> int:
         """The split size a staged step runs with (what mllm_plan_dev clamps it to)."""
         return max(self.SPLIT_MIN, min(128, int(pages_per_split)))
-
-    def records(self, seqs: list[SeqStep], pages_per_split: int) -> int:
-        """Decode plan records the step needs at its staged split size, padding rows included (one page
-        each)."""
-        bs = self.block_size
-        pages = sum(-(-(s.num_cached + 1) // bs) for s in seqs) + (self.num_rows - len(seqs))
-        return decode_plan_size(pages, self.num_rows, self.split_size(pages_per_split))[0]
 
     def load(self, keys, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
         """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host packing,
