@@ -183,6 +183,59 @@ def test_random_decode_heavy_steps(hip, seed):
     _check(*fp8_step(wl, rng.uniform(0.02, 0.5), rng.uniform(0.02, 0.5)))
 
 
+@pytest.mark.parametrize("h,hkv", [(32, 8), (21, 7)], ids=["pair-kernel", "one-head-kernel"])
+def test_decode_rows_with_pages_past_their_last_token(hip, h, hkv):
+    # the fp8 decode kernels' stream across a segment with no tile (a page list that runs past the row's
+    # last token): rows with 0-5 extra pages through mllm_paged_decode_fp8, against the oracle on the
+    # rows without them; 8 KV heads run the pair kernel, 7 the one-head kernel
+    import random
+
+    import decode_plan
+    from minillm import _native
+    from minillm.attention.hip_backend import _ptr
+    from minillm.attention.metadata import AttentionMetadata, SeqStep, decode_plan_size
+
+    rng = random.Random(23)
+    steps = [(rng.randrange(0, 300), 1) for _ in range(40)]
+    wl = _kernel_case(h=h, hkv=hkv, steps=steps, num_blocks=400, seed=23)
+    ks, vs = 0.05, 0.04
+    _, _, ref, (exp_k, exp_v) = fp8_step(wl, ks, vs)  # the oracle's output and pools after the append
+    extra = [rng.randrange(0, 6) for _ in steps]
+    lists = [list(b) + [rng.randrange(wl.num_blocks) for _ in range(e)] for (_, _, b), e in zip(wl.seqs, extra)]
+    c = 8
+    _, segs, _, _ = decode_plan.restate([(i, len(x), 0, i, cc + 1) for i, ((cc, _), x) in enumerate(zip(steps, lists))], c)
+    assert any(r0[2] * 16 >= r0[3] for r0, _ in segs)  # some segment holds extra pages only
+
+    meta = AttentionMetadata.build([SeqStep(cc, n, list(b)) for cc, n, b in wl.seqs], wl.block_size, DEV)
+    pk8, pv8 = exp_k.clone(), exp_v.clone()  # the pools after this step's append (checked by fp8_step)
+    q = wl.q.to(DEV)
+    kv_indptr = torch.tensor([0] + [sum(len(x) for x in lists[:i + 1]) for i in range(len(lists))],
+                             dtype=torch.int32, device=DEV)
+    kv_indices = torch.tensor([b for x in lists for b in x], dtype=torch.int32, device=DEV)
+    total = sum(len(x) for x in lists)
+    n_rec, n_merge = decode_plan_size(total, len(lists), c)
+    dec = torch.full((4 * n_rec,), -1, dtype=torch.int32, device=DEV)
+    mrg = torch.full((4 * n_merge,), -1, dtype=torch.int32, device=DEV)
+    lib = _native.lib()
+    st = _native.stream_ptr(DEV)
+    lib.call("mllm_plan", meta.qo_indptr.data_ptr(), kv_indptr.data_ptr(), meta.seq_lens_i32.data_ptr(), len(lists),
+             c, 64, dec.data_ptr(), n_rec, _ptr(mrg), n_merge, 0, 0, st)
+    ws = torch.empty(lib.workspace_bytes(n_rec, h, 128), dtype=torch.uint8, device=DEV)
+    out = torch.full_like(q, float("nan"))
+    nb, bs, _, dh = pk8.shape
+    lib.call("mllm_paged_decode_fp8", q.data_ptr(), q.stride(0), q.stride(1), pk8.data_ptr(), pv8.data_ptr(), nb, bs,
+             h, hkv, dh, meta.qo_indptr.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+             meta.seq_lens_i32.data_ptr(), dec.data_ptr(), n_rec, _ptr(mrg), n_merge, c, dh ** -0.5,
+             _native.dtype_code(q.dtype), ks, vs, out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(),
+             ws.numel(), st)
+    lib.call("mllm_merge_splits", _ptr(mrg), n_merge, n_rec, h, dh, meta.qo_indptr.data_ptr(),
+             _native.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), st)
+    torch.cuda.synchronize()
+    assert dec[0].item() == -(-total // c)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def _owned_slots(wl, include_new=True):
     used = torch.zeros(wl.num_blocks * wl.block_size, dtype=torch.bool)
     for c, n, blocks in wl.seqs:
