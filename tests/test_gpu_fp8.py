@@ -236,6 +236,34 @@ def test_decode_rows_with_pages_past_their_last_token(hip, h, hkv):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+def test_random_shapes_sweep(hip):
+    # 24 seeded steps over the whole shape space at once: 1-8 KV heads, 1-16 query heads per KV head, block
+    # sizes 16-128, 1-160 rows of decode and prefill rows, bf16 or fp8 pools (a third); each case is named
+    # before it runs
+    import random
+
+    from harness import hip_step, oracle_step
+
+    for i in range(24):
+        rng = random.Random(90000 + i)
+        hkv = rng.choice([1, 2, 4, 8])
+        g = rng.choice([1, 2, 4, 8] + ([16] if hkv <= 4 else []))
+        bs = rng.choice([16, 32, 64, 128])
+        fp8 = rng.random() < 0.35
+        steps = [(rng.randrange(0, rng.choice([20, 400, 3000])), 1 if rng.random() < 0.6 else rng.randrange(2, 300))
+                 for _ in range(rng.randrange(1, 160))]
+        nb = sum(-(-(c + n) // bs) for c, n in steps) + 4
+        print(f"sweep case {i}: h={hkv * g} hkv={hkv} bs={bs} fp8={fp8} rows={len(steps)}", flush=True)
+        wl = _kernel_case(h=hkv * g, hkv=hkv, bs=bs, steps=steps, num_blocks=nb, seed=i)
+        if fp8:
+            _check(*fp8_step(wl, rng.uniform(0.02, 0.5), rng.uniform(0.02, 0.5)))
+        else:
+            out, pk, pv, _ = hip_step(wl, DEV)
+            ref, rk, rv = oracle_step(wl, DEV)
+            assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+            torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def _owned_slots(wl, include_new=True):
     used = torch.zeros(wl.num_blocks * wl.block_size, dtype=torch.bool)
     for c, n, blocks in wl.seqs:
