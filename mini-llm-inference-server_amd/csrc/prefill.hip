@@ -6,8 +6,8 @@
 // times the G query heads that share the KV head: 256 MFMA rows, 32 per wavefront (rows are
 // token-major: row = token * G + head).  K and V stream through LDS in tiles of 64 keys, gathered
 // through kv_indices by direct global->LDS loads (global_load_lds_dwordx4: no VGPR staging) into two
-// rings, K four tiles deep and V three, so each tile's loads are issued four phases before its first
-// use.  A tile in LDS is its 64 key rows of the head, 256 bytes each, with the 16-byte chunks of row r
+// rings of four tiles each (128 KB), so each tile's loads are issued two 128-key phases before its
+// first use.  A tile in LDS is its 64 key rows of the head, 256 bytes each, with the 16-byte chunks of row r
 // XOR-swizzled (K: chunk ^ (r % 16); V: chunk ^ 4 (r % 4)) so that the MFMA operand reads below hit
 // distinct banks.
 // Per wavefront and K/V tile:
@@ -19,12 +19,12 @@
 // the PV product without leaving its lanes.  P^T's 16-key k-order is keys {4h..4h+3, 8+4h..8+4h+3}
 // (lane half h); the V^T reads pick their keys in the same order.
 //
-// The two halves of the workgroup run phase-shifted (see prefill_kernel): one half's matrix phase
+// The two halves of the workgroup run phase-shifted (prefill128_kernel): one half's matrix phase
 // coincides with the other half's softmax, so every SIMD has an MFMA stream and a vector stream at
-// once.  A phase covers two tiles (prefill128_kernel: 128 keys per phase, one softmax over both
-// score tiles); prefill_kernel, one tile per phase, is kept as a build option.  Tiles entirely above a
-// wavefront's causal diagonal are skipped.  Keys past the workgroup's last visible key are loaded as copies of that key's row (their scores are masked, so P is exactly
-// 0 and pool slots past a row's length are never read).  The grid is 1-D with the KV head fastest,
+// once.  A phase covers two tiles (128 keys, one softmax over both score tiles).  Tiles entirely above
+// a wavefront's causal diagonal are skipped.  Keys past the workgroup's last visible key are loaded as
+// copies of that key's row (their scores are masked, so P is exactly 0 and pool slots past a row's
+// length are never read).  The grid is 1-D with the KV head fastest,
 // so with 8 KV heads each XCD (workgroups are dealt round-robin to the 8 XCDs) serves one KV head and
 // keeps that head's shared-prefix pages in its own L2.
 //
@@ -44,17 +44,7 @@ constexpr int kHeadDim = 128;
 constexpr int kBN = 64;                      // keys per K/V tile
 constexpr int kRowBytes = kHeadDim * 2;      // one key row of the head in LDS
 constexpr int kTileBytes = kBN * kRowBytes;  // 16 KB
-constexpr int kRingK = 4;                    // K tiles in LDS
-constexpr int kRingV = 3;                    // V tiles in LDS
-constexpr int kVBase = kRingK * kTileBytes;  // byte offset of the V ring
-constexpr int kIdBase = (kRingK + kRingV) * kTileBytes;  // per wavefront two 64-entry windows of block ids
-constexpr int kLdsBytes = kIdBase + 8 * 2 * 64 * 4;
 constexpr int kQTileRows = 256;  // query rows (token x head of the group) per workgroup: 8 waves x 32
-// 1 (default): prefill128_kernel (128-key phases) for every pool type; 0: prefill_kernel (64-key phases)
-#ifndef MLLM_PREFILL_128
-#define MLLM_PREFILL_128 1
-#endif
-constexpr bool kPrefill128 = MLLM_PREFILL_128;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -80,10 +70,6 @@ struct PrefillArgs {
 // 8 w + 4 a + l / 16, physical chunk l % 16, and so fetches the logical chunk that the swizzle puts
 // there.  The group's block id is wave-uniform (a scalar load); for a full tile the address is a
 // 64-bit scalar base plus a per-lane offset that never changes.
-
-__device__ __forceinline__ int group_block(const PrefillArgs& a, const int32_t* pages, int key0, int last) {
-  return pages[min(key0, last) >> a.bs_shift];
-}
 
 // Pool address of slot key0 % bs of block `id` for this head's rows (uniform).
 __device__ __forceinline__ const char* group_base(const char* pool, const PrefillArgs& a, int id, int key0) {
@@ -142,16 +128,6 @@ __device__ __forceinline__ void stage_store(u32x4 x, int w, int lane, char* slot
   *reinterpret_cast<u32x4*>(row + 16 * ((c0 + 1) ^ sw)) = fp8x8_to<T>(x[2], x[3]);
 }
 
-// N = number of DMA instructions issued since the loads that must have landed (0, 2 or 4)
-__device__ __forceinline__ void barrier_vm_n(int n) {
-  if (n >= 4)
-    barrier_vm<4>();
-  else if (n >= 2)
-    barrier_vm<2>();
-  else
-    barrier_vm<0>();
-}
-
 // ---------------------------------------------------------------- MFMA operands from LDS
 
 __device__ __forceinline__ u32x2 ld_tr(const char* p) {
@@ -180,61 +156,6 @@ __device__ __forceinline__ STile scores(const char* lds, unsigned kb, const u32x
     t.s[1] = Mfma<T>::m32x32x16(ld16(p + 32 * kRowBytes), qf[kk], t.s[1]);
   }
   return t;
-}
-
-// Softmax of one score tile (online, exp2 domain) -> the bf16/fp16 P^T operands of its PV product.
-// Masks keys past each row's position when the tile reaches past the wavefront's first row; rescales
-// O and l lazily: only when some row's max grew by more than 2^8, otherwise p = 2^((s - m) c) stays
-// below 256, which the fp32 accumulation and the P operand hold as exactly as values below 1.
-template <typename T>
-__device__ __forceinline__ void softmax_tile(STile& st, u32x4 (&pf)[2][2], f32x16 (&oacc)[4], float& m_run,
-                                             float& l_run, int kv0, int qp, int wave_qp_lo, int h, float c) {
-  if (kv0 + kBN - 1 > wave_qp_lo) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-        st.s[b][r] = key > qp ? -INFINITY : st.s[b][r];
-      }
-  }
-  // row max: four independent chains (v_max3), then the other half of the row from lane l ^ 32
-  float m4[4] = {st.s[0][0], st.s[0][1], st.s[0][2], st.s[0][3]};
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = (b == 0 ? 4 : 0); r < 16; ++r) m4[r & 3] = __builtin_fmaxf(m4[r & 3], st.s[b][r]);
-  const float mx = max_xor32(__builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3])));
-  if (__any((mx - m_run) * c > 8.f)) {
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2((m_run - m_new) * c);
-    l_run *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
-    m_run = m_new;
-  }
-  const float mc = m_run * c;
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st.s[b][r] = fast_exp2(__builtin_fmaf(st.s[b][r], c, -mc));
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int r0 = 8 * u;
-      pf[b][u] = u32x4{pack2<T>(st.s[b][r0 + 0], st.s[b][r0 + 1]), pack2<T>(st.s[b][r0 + 2], st.s[b][r0 + 3]),
-                       pack2<T>(st.s[b][r0 + 4], st.s[b][r0 + 5]), pack2<T>(st.s[b][r0 + 6], st.s[b][r0 + 7])};
-    }
-  // row sum in fp32, four chains: plain adds, because the packed bf16 dot instructions do not run
-  // beside MFMAs (each stalls the SIMD partner's matrix phase); the unrounded sum differs from the sum of
-  // the rounded P operand by unbiased bf16 rounding noise only
-  float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s4[r & 3] += st.s[b][r];
-  l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
 }
 
 // O^T += V^T . P^T for one tile: 16 MFMAs, the four 32-dim output tiles as independent chains.
@@ -330,226 +251,15 @@ __device__ __forceinline__ void matrix_phase_pair(const char* lds, unsigned vb0,
   }
 }
 
+// ---------------------------------------------------------------- the kernel: 128-key phases
 // Two wavefront groups of one workgroup, phase-shifted by half an iteration: while group A (waves
 // 0-3) runs its matrix phase, group B (waves 4-7) runs its vector phase, and the next barrier swaps
 // them, so each SIMD (one wave of each group) keeps its matrix pipe and its vector ALU busy together.
-//   matrix phase i : O += V(i) P(i)  and  S(i+1) = K(i+1) Q^T
-//   vector phase   : P(i+1) = softmax(S(i+1)) (group B's vector phase runs half an iteration earlier)
-// Loads: at even phase 2s every wavefront issues its share of V(s+2) (into the slot of V(s-1)) and
-// K(s+3) (into the slot of K(s-1)), both freed by the barrier that ended phase 2s-1; the barrier that
-// ends phase 2s+1 waits for everything but those, so the tiles phase 2s+2 reads (K(s+2), V(s+1)) have
-// landed in every wavefront's share.
-template <typename T, bool F8>
-__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int grp = wave >> 2;  // 0: matrix phase first; 1: vector phase first
-  const int wu = __builtin_amdgcn_readfirstlane(wave);  // the same index, as a uniform value (load addressing)
-  const int kvh = blockIdx.x % a.Hkv;
-  // plan record {seq, t0, qs, nn, cached, kv_start, kv_end, ntiles}: new tokens t0 .. t0 + QT - 1 of row
-  // seq (qs: its first row in q; nn new tokens after `cached` cached ones; page ids from
-  // kv_indices[kv_start]); its rows see keys 0 .. kv_end - 1, ntiles 64-key tiles.  One scalar load.
-  const int4 w0 = a.work[2 * (blockIdx.x / a.Hkv)], w1 = a.work[2 * (blockIdx.x / a.Hkv) + 1];
-  const int seq = w0.x, t0 = w0.y, qs = w0.z, nn = w0.w, cached = w1.x;
-  // unfilled plan slot (the host pre-fills the plan with -1), or a row whose seq_lens did not cover its
-  // new tokens (no visible key: nothing to load; uniform, before any barrier)
-  if (seq < 0 || w1.z <= 0) return;
-  const int len = cached + nn;
-  const int32_t* pages = a.kv_indices + w1.y;
-  const int tpw = 32 / a.G;  // tokens per wavefront
-  const int kv_end = w1.z;   // keys any row of this workgroup may see
-  const int last = kv_end - 1;
-  const int ntiles = w1.w;
-
-  const int n = lane & 31, h = lane >> 5;
-  const int tok = t0 + wave * tpw + n / a.G;  // new-token index within the row
-  const bool row_valid = tok < nn;
-  const int qp = row_valid ? cached + tok : len - 1;  // context position of the row's token
-  const int wave_tok_hi = min(t0 + wave * tpw + tpw, nn) - 1;
-  const int wave_qp_hi = wave_tok_hi >= t0 + wave * tpw ? cached + wave_tok_hi : -1;  // -1: no valid row
-  const int wave_qp_lo = cached + t0 + wave * tpw;  // position of the wavefront's first row
-  const float c = a.scale_log2;
-
-  // load lanes: tile rows r0, r1 of this wavefront's two DMA instructions; offsets from the group base
-  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * (F8 ? 1 : 2));
-  const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
-  const unsigned rb = (unsigned)a.row_bytes;
-  const unsigned koff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * k_chunk(r0, lane);
-  const unsigned koff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * k_chunk(r1, lane);
-  const unsigned voff0 = (unsigned)(r0 & 15) * rb + head_bytes + 16u * v_chunk(r0, lane);
-  const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
-  const unsigned soff = (unsigned)(8 * (wave & 1) + (lane >> 3)) * rb + head_bytes + 16u * (lane & 7);  // fp8
-  // operand reads (see scores / pv_tile)
-  const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
-  const unsigned vread = (unsigned)(kVBase + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
-
-  const char* kc = reinterpret_cast<const char*>(a.kc);
-  const char* vc = reinterpret_cast<const char*>(a.vc);
-  const int g16 = 16 * (wu >> 1);  // first key of this wavefront's load group within a tile
-  auto k_slot = [&](int t) { return lds + (t & (kRingK - 1)) * kTileBytes; };
-  auto v_slot = [&](int t) { return lds + kVBase + (t % kRingV) * kTileBytes; };
-
-  // Block ids of this wavefront's load group, in windows of 64 tiles DMA'd into LDS (two per
-  // wavefront): entry j of the window holds the id for tile wbase + j.
-  const int* idwin = reinterpret_cast<const int*>(lds + kIdBase) + wu * 128;
-  auto load_ids = [&](int base, int sel) {
-    dma4(reinterpret_cast<const char*>(pages), 4u * (unsigned)(min((base + lane) * kBN + g16, last) >> a.bs_shift),
-         lds_offset(idwin + 64 * sel));
-  };
-  int wbase = 0, wsel = 0;
-  auto blk_of = [&](int t) { return __builtin_amdgcn_readfirstlane(idwin[64 * wsel + t - wbase]); };
-  load_ids(0, 0);
-  // the first three tiles take their block ids from scalar loads, so their loads need not wait for the
-  // id window
-  auto blk_direct = [&](int t) { return pages[min(t * kBN + g16, last) >> a.bs_shift]; };
-
-  f32x16 oacc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  // prologue: K(0), V(0), K(1), V(1), K(2), then Q; all of them have landed after the first barrier
-  if constexpr (F8) {
-    for (int t = 0; t < min(ntiles, 3); ++t) {
-      const int b = blk_direct(t);
-      const u32x4 kx = stage_load(kc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
-      if (t < 2) {
-        const u32x4 vx = stage_load(vc, a, b, t * kBN, last, kv_end, wu, soff, head_bytes, lane);
-        stage_store<T, true>(vx, wu, lane, v_slot(t));
-      }
-      stage_store<T, false>(kx, wu, lane, k_slot(t));
-    }
-    barrier_vm<0>();
-  } else {
-    {
-      const int b0 = blk_direct(0);
-      dma_tile<false>(kc, a, b0, 0, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(0));
-      dma_tile<true>(vc, a, b0, 0, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(0));
-    }
-    if (ntiles > 1) {
-      const int b1 = blk_direct(1);
-      dma_tile<false>(kc, a, b1, kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(1));
-      dma_tile<true>(vc, a, b1, kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(1));
-    }
-    if (ntiles > 2)
-      dma_tile<false>(kc, a, blk_direct(2), 2 * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(2));
-  }
-  // Q after the tile loads (its latency overlaps theirs); the wait for Q covers everything before it
-  u32x4 qf[8];  // Q^T operand: lane (n, h) holds row n at dims 16 kk + 8 h .. +7
-  {
-    const int head = kvh * a.G + (n % a.G);
-    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
-      qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
-    }
-  }
-  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
-               : "memory");
-  barrier_vm<0>();  // K(0), V(0), K(1), V(1), K(2), the id window and Q have landed
-
-  STile st;
-  u32x4 pf[2][2];
-  if (0 <= wave_qp_hi) {
-    st = scores<T>(lds, kread, qf);
-    if (grp == 0) softmax_tile<T>(st, pf, oacc, m_run, l_run, 0, qp, wave_qp_lo, h, c);
-  }
-
-  int issued = 0;  // DMA instructions of the last even phase
-  u32x4 kst = {0, 0, 0, 0}, vst = {0, 0, 0, 0};  // fp8: K(s+3), V(s+2) between their load and LDS store
-  for (int p = 0; p < 2 * ntiles; ++p) {
-    const int s = p >> 1;
-    if ((p & 1) == 0) {
-      const int vblk = blk_of(s + 2), kblk = blk_of(s + 3);
-      if (s + 4 >= wbase + 64) {  // the next even phase needs tile s + 4: move the window (its DMA goes
-        wsel ^= 1;                // out before this phase's tile loads, so the barrier that waits for
-        wbase = s + 3;            // those older loads covers it)
-        load_ids(wbase, wsel);
-      }
-      issued = 0;
-      if (s + 2 < ntiles) {
-        if constexpr (F8)
-          vst = stage_load(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, soff, head_bytes, lane);
-        else
-          dma_tile<true>(vc, a, vblk, (s + 2) * kBN, last, kv_end, wu, voff0, voff1, head_bytes, lane, v_slot(s + 2));
-        issued += 2;
-      }
-      if (s + 3 < ntiles) {
-        if constexpr (F8)
-          kst = stage_load(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, soff, head_bytes, lane);
-        else
-          dma_tile<false>(kc, a, kblk, (s + 3) * kBN, last, kv_end, wu, koff0, koff1, head_bytes, lane, k_slot(s + 3));
-        issued += 2;
-      }
-    }
-    if ((p & 1) == grp) {  // matrix phase s, at raised wave priority so its MFMAs issue first on the SIMD
-      __builtin_amdgcn_s_setprio(1);
-      const unsigned vb = vread + (s % kRingV) * kTileBytes, kb = kread + ((s + 1) & (kRingK - 1)) * kTileBytes;
-      const bool do_pv = s * kBN <= wave_qp_hi, do_s = s + 1 < ntiles && (s + 1) * kBN <= wave_qp_hi;
-      if (do_pv && do_s) {
-        matrix_phase<T>(lds, vb, kb, pf, oacc, st, qf);
-      } else {
-        if (do_pv) pv_tile<T>(lds, vb, pf, oacc);
-        if (do_s) st = scores<T>(lds, kb, qf);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    } else {  // vector phase: softmax of S(j)
-      const int j = (p + 1) >> 1;
-      if (j < ntiles && j * kBN <= wave_qp_hi) softmax_tile<T>(st, pf, oacc, m_run, l_run, j * kBN, qp, wave_qp_lo, h, c);
-    }
-    if (p & 1) {
-      if constexpr (F8) {  // the slots of V(s-1) and K(s-1) are free since the barrier that ended phase 2s-1
-        if (s + 2 < ntiles) stage_store<T, true>(vst, wu, lane, v_slot(s + 2));
-        if (s + 3 < ntiles) stage_store<T, false>(kst, wu, lane, k_slot(s + 3));
-        barrier_vm<0>();
-      } else {
-        barrier_vm_n(issued);
-      }
-    } else {
-      barrier_lds();
-    }
-  }
-
-  // Output through LDS (the rings are idle after the loop's last barrier): the wavefront writes its 32
-  // rows x 128 dims into its own 8 KB, row-major with 16-byte chunk c of row r at chunk c ^ (r % 16),
-  // then stores whole 16-byte chunks, four rows per instruction (one token's G heads are adjacent rows,
-  // contiguous in out for the usual head stride).  Scattered 8-byte partial-line stores kept the
-  // workgroup from retiring for several microseconds.
-  const float inv = (F8 ? a.v_scale : 1.f) / l_run;
-  char* ost = lds + wave * (32 * kRowBytes);
-  // oacc[dt][r]: dim 32 dt + 8 (r / 4) + 4 h + r % 4 of row n, i.e. chunk 4 dt + r / 4, half h
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int r = 4 * g4;
-      const u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
-                             pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
-      *reinterpret_cast<u32x2*>(ost + n * kRowBytes + 16 * ((4 * dt + g4) ^ (n & 15)) + 8 * h) = pk;
-    }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 4 * i + (lane >> 4), chunk = lane & 15;  // lane's row of the wavefront and its chunk
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + row * kRowBytes + 16 * (chunk ^ (row & 15)));
-    const int rtok = t0 + wave * tpw + row / a.G;
-    if (rtok < nn) {
-      uint16_t* o = a.out + (int64_t)(qs + rtok) * a.o_st + (int64_t)(kvh * a.G + row % a.G) * a.o_sh;
-      *reinterpret_cast<u32x4*>(o + 8 * chunk) = v;
-    }
-  }
-}
-
-// ---------------------------------------------------------------- 128-key phases
-// The same workgroup, tiles and operand layouts as prefill_kernel, but every phase covers two 64-key
-// tiles (a pair): the matrix phase of pair j runs PV of tiles 2j and 2j+1 and S of tiles 2j+2 and 2j+3
-// (64 MFMAs), and the vector phase runs one softmax over both score tiles (one max and one rescale
-// test per 128 keys).  Half the phases means half the barriers and per-phase bookkeeping per key:
-// prefix_64 674 us against 702-716 us for 64-key phases, mixed_128 76 against 78-80 us (same box).
+// Every phase covers two 64-key tiles (a pair): the matrix phase of pair j runs PV of tiles 2j and
+// 2j+1 and S of tiles 2j+2 and 2j+3 (64 MFMAs), and the vector phase runs one softmax over both score
+// tiles (one max and one rescale test per 128 keys).  Against phases of one tile (a design measured
+// and replaced), half the phases means half the barriers and per-phase bookkeeping per key:
+// prefix_64 674 us against 702-716 us, mixed_128 76 against 78-80 us (same box).
 // When all four products of a pair run, they are one 64-MFMA sequence with one operand ring
 // (matrix_phase_pair), so the second tile's first operands are read under the first tile's last
 // MFMAs: another 1.3% on prefix_64 (649 against 657-659 us), bit-identical.
@@ -561,15 +271,21 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 // fp8 pools: V(2j+2), V(2j+3) are loaded into VGPRs at the start of phase 2j and K(2j+4), K(2j+5) at
 // the start of phase 2j+1, each pair widened into LDS at the end of its phase (the slots are free
 // since the barrier that ended phase 2j-1).  The eight staging VGPRs leave no room for the pair's
-// single operand ring, so fp8 pools run the two tiles' products one after the other.  Against the
-// 64-key kernel on fp8 pools: prefix_64 725 against 756 us, mixed_128 82 against 87 us (same box).
-constexpr int kRingK2 = 4, kRingV2 = 4;  // K and V tiles in LDS
-constexpr int kVBase2 = kRingK2 * kTileBytes;
-constexpr int kIdBase2 = (kRingK2 + kRingV2) * kTileBytes;
-constexpr int kLdsBytes2 = kIdBase2 + 8 * 2 * 64 * 4;
+// single operand ring, so fp8 pools run the two tiles' products one after the other.  Against phases
+// of one tile on fp8 pools: prefix_64 725 against 756 us, mixed_128 82 against 87 us (same box).
+constexpr int kRingK = 4, kRingV = 4;  // K and V tiles in LDS
+constexpr int kVBase = kRingK * kTileBytes;
+constexpr int kIdBase = (kRingK + kRingV) * kTileBytes;
+constexpr int kLdsBytes = kIdBase + 8 * 2 * 64 * 4;
 
-// Online softmax of a pair of score tiles (keys kv0 .. kv0 + 127) -> the P^T operands of both PV
-// products, as softmax_tile does for one tile.
+// Online softmax (exp2 domain) of a pair of score tiles (keys kv0 .. kv0 + 127) -> the bf16/fp16 P^T
+// operands of both PV products.  Masks keys past each row's position when the pair reaches past the
+// wavefront's first row; rescales O and l lazily: only when some row's max grew by more than 2^8,
+// otherwise p = 2^((s - m) c) stays below 256, which the fp32 accumulation and the P operand hold as
+// exactly as values below 1.  Row max and row sum run as four chains each (v_max3, plain adds), then
+// the other half of the row comes from lane l ^ 32.  The sum is taken over the unrounded p with plain
+// adds, because the packed bf16 dot instructions do not run beside MFMAs (each stalls the SIMD
+// partner's matrix phase); it differs from the sum of the rounded P operand by unbiased rounding noise.
 template <typename T>
 __device__ __forceinline__ void softmax_two(STile& s0, STile& s1, u32x4 (&pf0)[2][2], u32x4 (&pf1)[2][2],
                                             f32x16 (&oacc)[4], float& m_run, float& l_run, int kv0, int qp,
@@ -632,7 +348,7 @@ __device__ __forceinline__ void softmax_two(STile& s0, STile& s1, u32x4 (&pf0)[2
 
 template <typename T, bool F8>
 __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes2];
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -668,15 +384,15 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
   const unsigned voff1 = (unsigned)(r1 & 15) * rb + head_bytes + 16u * v_chunk(r1, lane);
   const unsigned soff = (unsigned)(8 * (wave & 1) + (lane >> 3)) * rb + head_bytes + 16u * (lane & 7);  // fp8
   const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
-  const unsigned vread = (unsigned)(kVBase2 + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
+  const unsigned vread = (unsigned)(kVBase + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
 
   const char* kc = reinterpret_cast<const char*>(a.kc);
   const char* vc = reinterpret_cast<const char*>(a.vc);
   const int g16 = 16 * (wu >> 1);
-  auto k_slot = [&](int t) { return lds + (t & (kRingK2 - 1)) * kTileBytes; };
-  auto v_slot = [&](int t) { return lds + kVBase2 + (t & (kRingV2 - 1)) * kTileBytes; };
+  auto k_slot = [&](int t) { return lds + (t & (kRingK - 1)) * kTileBytes; };
+  auto v_slot = [&](int t) { return lds + kVBase + (t & (kRingV - 1)) * kTileBytes; };
 
-  const int* idwin = reinterpret_cast<const int*>(lds + kIdBase2) + wu * 128;
+  const int* idwin = reinterpret_cast<const int*>(lds + kIdBase) + wu * 128;
   auto load_ids = [&](int base, int sel) {
     dma4(reinterpret_cast<const char*>(pages), 4u * (unsigned)(min((base + lane) * kBN + g16, last) >> a.bs_shift),
          lds_offset(idwin + 64 * sel));
@@ -783,14 +499,14 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
       // all four products of the pair (fp8 pools keep two tiles of staging registers: no single ring)
       const bool full = !F8 && ta + 3 < ntiles && (ta + 3) * kBN <= wave_qp_hi;
       if (full) {
-        matrix_phase_pair<T>(lds, vread + (ta & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 2) & (kRingK2 - 1)) * kTileBytes,
-                             vread + ((ta + 1) & (kRingV2 - 1)) * kTileBytes, kread + ((ta + 3) & (kRingK2 - 1)) * kTileBytes,
+        matrix_phase_pair<T>(lds, vread + (ta & (kRingV - 1)) * kTileBytes, kread + ((ta + 2) & (kRingK - 1)) * kTileBytes,
+                             vread + ((ta + 1) & (kRingV - 1)) * kTileBytes, kread + ((ta + 3) & (kRingK - 1)) * kTileBytes,
                              pf0, pf1, oacc, st0, st1, qf);
       } else
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int tv = ta + u, tk = ta + 2 + u;
-        const unsigned vb = vread + (tv & (kRingV2 - 1)) * kTileBytes, kb = kread + (tk & (kRingK2 - 1)) * kTileBytes;
+        const unsigned vb = vread + (tv & (kRingV - 1)) * kTileBytes, kb = kread + (tk & (kRingK - 1)) * kTileBytes;
         const bool do_pv = tv < ntiles && tv * kBN <= wave_qp_hi, do_s = tk < ntiles && tk * kBN <= wave_qp_hi;
         STile& st = u ? st1 : st0;
         const u32x4 (&pf)[2][2] = u ? pf1 : pf0;
@@ -910,30 +626,16 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.o_sh = out_stride_head;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
-  if (kPrefill128) {
-    if (dtype == MLLM_DTYPE_BF16) {
-      if (fp8)
-        prefill128_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
-      else
-        prefill128_kernel<BF16, false><<<grid, 512, 0, st>>>(a);
-    } else {
-      if (fp8)
-        prefill128_kernel<F16, true><<<grid, 512, 0, st>>>(a);
-      else
-        prefill128_kernel<F16, false><<<grid, 512, 0, st>>>(a);
-    }
-    return check_launch(fn.c_str());
-  }
   if (dtype == MLLM_DTYPE_BF16) {
     if (fp8)
-      prefill_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
+      prefill128_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
     else
-      prefill_kernel<BF16, false><<<grid, 512, 0, st>>>(a);
+      prefill128_kernel<BF16, false><<<grid, 512, 0, st>>>(a);
   } else {
     if (fp8)
-      prefill_kernel<F16, true><<<grid, 512, 0, st>>>(a);
+      prefill128_kernel<F16, true><<<grid, 512, 0, st>>>(a);
     else
-      prefill_kernel<F16, false><<<grid, 512, 0, st>>>(a);
+      prefill128_kernel<F16, false><<<grid, 512, 0, st>>>(a);
   }
   return check_launch(fn.c_str());
 }
