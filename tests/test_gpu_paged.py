@@ -569,3 +569,27 @@ def test_maximum_sizes(hip, kv):
         assert torch.equal(pools[1].view(torch.uint8), exp[1].view(torch.uint8))
     assert torch.isfinite(out).all()
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+def test_stream_handle_is_the_current_stream():
+    """Every launch goes on the raw stream `_native.stream_ptr` returns: torch's current stream of the device
+    (the default one, a side stream inside `torch.cuda.stream`, and the capture stream of a graph being
+    recorded), whatever form the device is given in."""
+    from minillm import _native
+
+    dev = torch.device(DEV)
+    want = torch.cuda.current_stream(dev).cuda_stream
+    assert _native.stream_ptr(dev) == _native.stream_ptr(DEV) == _native.stream_ptr(0) == want
+    assert _native.stream_ptr(torch.device("cuda")) == want
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        assert _native.stream_ptr(dev) == side.cuda_stream != want
+    x = torch.zeros(4, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got, cap = _native.stream_ptr(dev), torch.cuda.current_stream(dev).cuda_stream
+        x.add_(1)
+    assert got == cap != want
+    graph.replay()
+    torch.cuda.synchronize()
+    assert x.tolist() == [1.0] * 4
