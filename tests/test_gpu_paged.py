@@ -571,6 +571,24 @@ def test_maximum_sizes(hip, kv):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+def test_rows_without_new_tokens(hip):
+    """Rows with no new token, which the reference's build accepts (metadata.py:70-103) and its
+    multi-token loop attends with zero queries (paged_torch_ref.py:61-73): the metadata is bit-identical
+    to the oracle's (a first row without tokens has logits_index -1), the pools too, and every new token's
+    output matches the oracle."""
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    steps = [(40, 0), (37, 1), (100, 0), (0, 5), (300, 1), (17, 0), (64, 33), (250, 0), (129, 1)]
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=96, seed=5)
+    meta = AttentionMetadata.build([SeqStep(c, n, b) for c, n, b in wl.seqs], wl.block_size, DEV)
+    _meta_fields_equal(meta, build_metadata([OracleSeq(c, n, list(b)) for c, n, b in wl.seqs], wl.block_size))
+    assert meta.logits_index[0].item() == -1
+    out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
 def test_stream_handle_is_the_current_stream():
     """Every launch goes on the raw stream `_native.stream_ptr` returns: torch's current stream of the device
     (the default one, a side stream inside `torch.cuda.stream`, and the capture stream of a graph being

@@ -459,3 +459,33 @@ def test_fp8_paged_attention_equals_textbook_over_dequantized_context():
         exp = naive_attention(q[st:st + n].transpose(0, 1), dk.transpose(0, 1), dv.transpose(0, 1),
                               causal_allowed(n, length))
         torch.testing.assert_close(out[st:st + n].double(), exp.transpose(0, 1), atol=1e-5, rtol=1e-5)
+
+
+def test_rows_without_new_tokens_attend_nothing():
+    """A row with no new token, which the reference's build accepts (metadata.py:70-103) and its
+    multi-token loop attends with zero queries (paged_torch_ref.py:61-73), adds no output row and leaves
+    every other row's output bit-identical to the same step without it; its logits_index is
+    starts[i + 1] - 1, so -1 when it comes first."""
+    g = torch.Generator().manual_seed(11)
+    h, hkv, dh, bs, nblk = 4, 2, 16, 4, 64
+    rows = [(5, 1), (0, 6), (9, 3), (13, 1), (7, 0), (12, 0), (3, 0)]  # the last three have no new token
+    pool_k = torch.randn(nblk, bs, hkv, dh, generator=g)
+    pool_v = torch.randn(nblk, bs, hkv, dh, generator=g)
+    perm = torch.randperm(nblk, generator=g).tolist()
+    blocks = [[perm.pop() for _ in range(-(-(c + n) // bs))] for c, n in rows]
+    ntok = sum(n for _, n in rows)
+    q = torch.randn(ntok, h, dh, generator=g)
+    k = torch.randn(ntok, hkv, dh, generator=g)
+    v = torch.randn(ntok, hkv, dh, generator=g)
+
+    def run(order):
+        meta = build_metadata([OracleSeq(*rows[i], blocks[i]) for i in order], bs)
+        out = torch_ref.forward(q, k, v, pool_k.clone(), pool_v.clone(), torch_ref.torch_meta(meta, "cpu"))
+        return out, meta
+
+    out_a, _ = run([0, 1, 2, 3])
+    out_b, meta_b = run([4, 0, 5, 1, 2, 6, 3])
+    assert out_b.shape == (ntok, h, dh)
+    assert torch.equal(out_a, out_b)
+    assert meta_b.query_start_loc == [0, 0, 1, 1, 7, 10, 10, 11]
+    assert meta_b.logits_index.tolist() == [-1, 0, 0, 6, 9, 9, 10]
