@@ -215,3 +215,86 @@ def test_prefix_cache_changes_no_token(hip):
     assert_greedy_match(on, off)
     assert_greedy_match(tight, off)
     assert core.stats().prefix_cache_hits > 0 and core_t.stats().prefix_cache_hits > 0
+
+
+def _pick(row):
+    """Greedy token of a logits row and its top-1 - top-2 margin in ulps of the row's dtype (as run_engine)."""
+    top2 = row.float().topk(2).values
+    ulp = torch.finfo(row.dtype).eps * top2[0].abs().clamp_min(1.0)
+    return int(row.argmax()), float((top2[0] - top2[1]) / ulp)
+
+
+@torch.no_grad()
+def _run_paged(model, backend, ps, steps, chunk_first=None, num_blocks=64):
+    """The reference's hand-driven ragged run (tests/test_paged.py:99-136) on the GPU: one ragged step for
+    every sequence each time, blocks scattered at random and the pool filled with 1e4 beforehand, so reading
+    any slot a sequence does not own changes its logits; `chunk_first` prefills that many tokens of every
+    prompt first, then the rest on top of them.  Returns per sequence [(token, margin)]."""
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+    from minillm.cache.paged import PagedKVCache
+
+    bs = 16
+    model.set_backend(backend)
+    cache = PagedKVCache(model.config, num_blocks, DEV, next(model.parameters()).dtype)
+    for buf in cache.k + cache.v:
+        buf.fill_(1e4)
+    free = list(range(num_blocks))
+    random.Random(2).shuffle(free)
+    tokens, blocks, cached = [list(p) for p in ps], [[] for _ in ps], [0] * len(ps)
+    gen = [[] for _ in ps]
+    while min(len(g) for g in gen) < steps:
+        upto = [len(t) for t in tokens]
+        if chunk_first and not any(cached):
+            upto = [min(chunk_first, len(t)) for t in tokens]
+        for i, b in enumerate(blocks):
+            while len(b) * bs < upto[i]:
+                b.append(free.pop())
+        meta = AttentionMetadata.build([SeqStep(cached[i], upto[i] - cached[i], blocks[i]) for i in range(len(ps))],
+                                       bs, DEV)
+        ids = torch.tensor([[t for i, tok in enumerate(tokens) for t in tok[cached[i]:upto[i]]]], device=DEV)
+        logits = model(ids, kv_cache=cache.step(meta), last_index=meta.logits_index)
+        assert torch.isfinite(logits).all()
+        for i in range(len(ps)):
+            if upto[i] < len(tokens[i]):  # mid-prompt chunk: nothing sampled yet
+                cached[i] = upto[i]
+                continue
+            cached[i] = len(tokens[i])
+            tok, margin = _pick(logits[i, -1])
+            tokens[i].append(tok)
+            gen[i].append((tok, margin))
+    return gen
+
+
+@torch.no_grad()
+def _greedy_no_cache(model, backend, p, steps):
+    """Batch-1 greedy generation that runs the model over the whole sequence every step (the reference's
+    generate.py:12-36), here with the contiguous attention of `backend`.  Returns [(token, margin)]."""
+    model.set_backend(backend)
+    ids, out = list(p), []
+    for _ in range(steps):
+        tok, margin = _pick(model(torch.tensor([ids], device=DEV))[0, -1])
+        ids.append(tok)
+        out.append((tok, margin))
+    return out
+
+
+def _prompt(seed, n):
+    return torch.randint(3, 256, (n,), generator=torch.Generator().manual_seed(seed)).tolist()
+
+
+@pytest.mark.parametrize("chunk_first", [None, 13])
+def test_ragged_paged_generation_matches_batch_1(hip, chunk_first):
+    # reference tests/test_paged.py:139-151: ragged paged generation over a 1e4-filled pool equals batch-1
+    # greedy generation, also when every prompt's first prefill is cut into a chunk and the rest on top;
+    # here the HIP ragged path against batch-1 generation with the oracle's float32 attention (a
+    # divergence is accepted only at a near-tie of the oracle's logits, as in the engine tests)
+    from minillm.attention import get_backend
+
+    model = tiny_model(seed=3)
+    if chunk_first:
+        ps, steps = [_prompt(5, 30), _prompt(6, 21)], 8
+    else:
+        ps, steps = [_prompt(1, 3), _prompt(2, 17), _prompt(3, 1), _prompt(4, 40)], 20  # 40 tokens: three blocks
+    got = _run_paged(model, get_backend("hip"), ps, steps, chunk_first=chunk_first)
+    exp = {f"s{i}": _greedy_no_cache(model, OracleBackend(), p, steps) for i, p in enumerate(ps)}
+    assert_greedy_match({f"s{i}": g[:steps] for i, g in enumerate(got)}, exp)

@@ -233,12 +233,12 @@ def test_reference_decode_only_step(hip):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("h,hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (32, 1)], ids=["g1", "g2", "g8", "g16", "g32"])
+@pytest.mark.parametrize("h,hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (4, 1), (16, 1), (32, 1)],
+                         ids=["g1", "g2", "g8", "g16", "mqa-g4", "mqa-g16", "g32"])
 def test_group_sizes(hip, h, hkv):
     steps = [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (17, 70)]
     wl = _kernel_case(h=h, hkv=hkv, steps=steps)
     if h // hkv > 16:  # decode supports up to 16 query heads per KV head
-        wl.seqs = [s for s in wl.seqs]
         with pytest.raises(ValueError, match="16 query heads"):
             hip_step(wl, DEV)
         return
