@@ -69,6 +69,10 @@ class StepPlan:
     merge_work: torch.Tensor
     prefill_work: torch.Tensor
     workspace_bytes: int
+    # the step's fixed pointer arguments, taken once per plan instead of once per layer: the metadata's
+    # qo_indptr, kv_indptr, kv_indices, seq_lens_i32, then the work lists and their sizes
+    meta_ptrs: tuple = ()
+    decode_args: tuple = ()
 
 
 def _ptr(t: torch.Tensor | None) -> int:
@@ -246,9 +250,7 @@ class HipBackend(AttentionBackend):
         num_blocks, bs, hkv, dh = k_cache.shape
         ws = self._workspace_for(plan.workspace_bytes, q.device)
         args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, bs,
-                q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(),
-                meta.seq_lens_i32.data_ptr(), _ptr(plan.decode_work), plan.num_decode, _ptr(plan.merge_work),
-                plan.num_merge, plan.pages_per_split, dh ** -0.5, _native.dtype_code(q.dtype))
+                q.shape[1], hkv, dh, *plan.decode_args, dh ** -0.5, _native.dtype_code(q.dtype))
         tail = (out.data_ptr(), out.stride(0), out.stride(1), _ptr(ws), plan.workspace_bytes,
                 _native.stream_ptr(q.device))
         if is_fp8(k_cache):
@@ -262,7 +264,7 @@ class HipBackend(AttentionBackend):
         if not plan.num_merge:
             return
         self._lib.call("mllm_merge_splits", _ptr(plan.merge_work), plan.num_merge, plan.num_decode, q.shape[1],
-                       q.shape[2], meta.qo_indptr.data_ptr(), _native.dtype_code(q.dtype), out.data_ptr(),
+                       q.shape[2], plan.meta_ptrs[0], _native.dtype_code(q.dtype), out.data_ptr(),
                        out.stride(0), out.stride(1), _ptr(self._workspace), plan.workspace_bytes,
                        _native.stream_ptr(q.device))
 
@@ -271,9 +273,8 @@ class HipBackend(AttentionBackend):
         plan = self._plan
         num_blocks, bs, hkv, dh = k_cache.shape
         args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, bs,
-                q.shape[1], hkv, dh, meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(),
-                meta.seq_lens_i32.data_ptr(), _ptr(plan.prefill_work), plan.num_prefill, plan.q_tile, dh ** -0.5,
-                _native.dtype_code(q.dtype))
+                q.shape[1], hkv, dh, *plan.meta_ptrs, _ptr(plan.prefill_work), plan.num_prefill, plan.q_tile,
+                dh ** -0.5, _native.dtype_code(q.dtype))
         tail = (out.data_ptr(), out.stride(0), out.stride(1), _native.stream_ptr(q.device))
         if is_fp8(k_cache):
             self._lib.call("mllm_paged_prefill_fp8", *args, k_scale, v_scale, *tail)
@@ -306,7 +307,10 @@ class HipBackend(AttentionBackend):
                            meta.seq_lens_i32.data_ptr(), meta.num_seqs, c, q_tile, _ptr(dec), n_dec, _ptr(mrg), n_merge,
                            _ptr(pf), n_pf, stream)
         ws = self._lib.workspace_bytes(n_dec, h, dh) if n_merge else 0
-        self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws)
+        meta_ptrs = (meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.kv_indices.data_ptr(),
+                     meta.seq_lens_i32.data_ptr())
+        self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws, meta_ptrs,
+                              (*meta_ptrs, _ptr(dec), n_dec, _ptr(mrg), n_merge, c))
         self._planned, self._planned_fp8 = meta, kv_fp8
 
     def _workspace_for(self, nbytes: int, dev) -> torch.Tensor | None:
