@@ -193,7 +193,7 @@ int mllm_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
 
 /*
  * Log-sum-exp merge of the split-KV partials mllm_paged_decode left in the workspace, one
- * {seq, first_item, num_splits} merge item (mllm_plan) per row with several splits:
+ * {seq, first partial slot, segments, 0} merge item (mllm_plan) per row cut into several segments:
  *   out = sum_j 2^(m_j - M) acc_j / sum_j 2^(m_j - M) l_j,  M = max_j m_j   (exp2 domain).
  * This is the same combine FlashInfer's split-KV decode performs after its chunks.
  */
