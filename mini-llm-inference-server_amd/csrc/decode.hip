@@ -640,7 +640,7 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
 }
 
 // Occupancy, tuned on MI355X (decode_256): every kernel loads one 16-token tile ahead of the one it
-// consumes.  The 16-bit kernel runs 3 wavefronts per SIMD (4 spills).  With per-row splits, one tile
+// consumes.  The 16-bit kernel runs 3 wavefronts per SIMD (160 VGPRs, no spills).  With per-row splits, one tile
 // of lookahead at 3 per SIMD streamed as fast as two at 2 per SIMD, and the fp8 pair kernel ran the same
 // with one tile ahead as with two (192-195 us); the fp8 one-head kernel then ran 198 us with four tiles
 // ahead at 2 per SIMD against 205 us with one at 4.
