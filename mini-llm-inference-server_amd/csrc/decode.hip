@@ -592,31 +592,37 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   }
 }
 
-// Log-sum-exp merge of a cut row's partials (one per segment): one workgroup per (row, head), one thread
-// per dim.
+// Log-sum-exp merge of a cut row's partials (one per segment).  One workgroup of 256 threads per (row, 8
+// heads): 32 threads per head, 4 dims per thread, so a row's partials of 8 heads arrive as 16-byte loads
+// in one round trip and a 256-row step launches 4 workgroups per cut row instead of 32.  Each output
+// element goes through the same operations, in the same order, as with one thread per (head, dim).
+constexpr int kMergeThreads = 256;
+constexpr int kMergeHeads = kMergeThreads / (kHeadDim / 4);  // heads per workgroup: 8
 template <typename T>
-__global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict__ merge, const float* __restrict__ part_o,
-                                                         const float2* __restrict__ part_ml, int H,
-                                                         const int32_t* __restrict__ qo_indptr, uint16_t* __restrict__ out,
-                                                         int64_t o_st, int64_t o_sh) {
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(const int4* __restrict__ merge,
+                                                             const float* __restrict__ part_o,
+                                                             const float2* __restrict__ part_ml, int H,
+                                                             const int32_t* __restrict__ qo_indptr,
+                                                             uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh) {
   const int4 mw = merge[blockIdx.x];
   const int seq = mw.x, first = mw.y, n = mw.z;
   if (seq < 0) return;
-  const int head = blockIdx.y;
-  const int d = threadIdx.x;
+  const int head = blockIdx.y * kMergeHeads + (int)(threadIdx.x >> 5);
+  if (head >= H) return;
+  const int d0 = 4 * (threadIdx.x & 31);
   // one online pass over the partials, four at a time so that their loads are in flight together (a row
   // has a few: one round trip instead of two per partial); slots past n re-read partial 0 of the
   // group and weigh it 2^-inf = 0
   constexpr int kGroup = 4;
-  float m = -INFINITY, lsum = 0.f, acc = 0.f;
+  float m = -INFINITY, lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int j0 = 0; j0 < n; j0 += kGroup) {
     float2 ml[kGroup];
-    float o[kGroup];
+    f32x4 o[kGroup];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
       const int64_t row = (int64_t)(first + (j0 + u < n ? j0 + u : j0)) * H + head;
       ml[u] = part_ml[row];
-      o[u] = part_o[row * kHeadDim + d];
+      o[u] = *reinterpret_cast<const f32x4*>(part_o + row * kHeadDim + d0);
     }
     float mc = m;
 #pragma unroll
@@ -626,17 +632,21 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(const int4* __restrict_
     }
     const float sc = fast_exp2(m - mc);  // 0 for the first group (m = -inf, lsum = acc = 0)
     lsum *= sc;
-    acc *= sc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= sc;
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
       const float wgt = fast_exp2(ml[u].x - mc);
       lsum += wgt * ml[u].y;
-      acc += wgt * o[u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += wgt * o[u][e];
     }
     m = mc;
   }
   const int qtok = qo_indptr[seq];
-  out[(int64_t)qtok * o_st + (int64_t)head * o_sh + d] = cvt1<T>(acc / lsum);
+  uint16_t* op = out + (int64_t)qtok * o_st + (int64_t)head * o_sh + d0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) op[e] = cvt1<T>(acc[e] / lsum);
 }
 
 // Occupancy, tuned on MI355X (decode_256): every kernel loads one 16-token tile ahead of the one it
@@ -807,14 +817,14 @@ int launch_merge(const int32_t* merge_work, int32_t num_merge_work, int32_t num_
   const float* part_o = static_cast<const float*>(workspace);
   const float2* part_ml = reinterpret_cast<const float2*>(static_cast<const char*>(workspace) +
                                                           (int64_t)num_decode_work * num_heads * kHeadDim * 4);
-  dim3 grid(num_merge_work, num_heads);
+  dim3 grid(num_merge_work, (num_heads + kMergeHeads - 1) / kMergeHeads);
   const int4* merge = reinterpret_cast<const int4*>(merge_work);
   if (dtype == MLLM_DTYPE_BF16)
-    merge_kernel<BF16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
-                                                  static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+    merge_kernel<BF16><<<grid, kMergeThreads, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                       static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
   else
-    merge_kernel<F16><<<grid, kHeadDim, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
-                                                 static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
+    merge_kernel<F16><<<grid, kMergeThreads, 0, st>>>(merge, part_o, part_ml, num_heads, qo_indptr,
+                                                      static_cast<uint16_t*>(out), out_stride_tok, out_stride_head);
   return check_launch("mllm_merge_splits");
 }
 
