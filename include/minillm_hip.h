@@ -130,7 +130,7 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  *     nb = ceil(T / pages_per_split) bins; bin b holds pages floor(b T / nb) .. floor((b + 1) T / nb) - 1
  *     (stream-K: one decode workgroup per bin, equal work for every wavefront).  A row's part inside a
  *     bin is a segment.  decode_work[num_decode_work] (int4 records) receives:
- *       [0]                       {nb, segments, partial slots, 0}
+ *       [0]                       {nb, segments, partial slots, 0} (overflow: {0, records, merges, -1})
  *       [1 + b]                   {first segment, end segment, 1 + nb, -} of bin b
  *       [1 + nb + 2 g], [.. + 1]  segment g: {first page's index in kv_indices, pages, first page within
  *                                 the row, row length}, {qo_indptr[seq], partial slot or -1, seq, 0}
@@ -142,11 +142,14 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  *     {seq, first_new_token, qo_indptr[seq], new tokens of seq, cached tokens of seq, kv_indptr[seq],
  *      keys visible to the tile's last token, 64-key tiles they span} -> prefill_work[8 * num_prefill_work],
  *     across all rows in decreasing number of those tiles (the prefill kernel's work per item).
- * The caller computes the three capacities from the same host facts (sequence lengths and new-token
- * counts) and fills the buffers with -1 beforehand.  A step whose decode plan does not fit
- * num_decode_work records or num_merge_work merges gets no decode work at all (the header reads nb = 0),
- * so the decode and merge kernels never index past a workspace sized for num_decode_work partial slots.
- * Prefill items past num_prefill_work are dropped.  pages_per_split <= 128.
+ * The caller computes the capacities from the facts the plan itself counts: the decode rows' page
+ * counts kv_indptr[s + 1] - kv_indptr[s] (which may exceed ceil(seq_len / block_size) when a page list
+ * runs past the row's last token), the number of decode rows, and the new-token counts; it fills the
+ * buffers with -1 beforehand.  A step whose decode plan does not fit num_decode_work records or
+ * num_merge_work merges gets no decode work at all: the header then reads {0, records needed, merges
+ * needed, -1} (a step with no decode pages reads {0, 0, 0, 0}), so the decode and merge kernels never
+ * index past a workspace sized for num_decode_work partial slots, and a caller that reads the header
+ * sees the overflow.  Prefill items past num_prefill_work are dropped.  pages_per_split <= 128.
  */
 int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
               int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,

@@ -163,8 +163,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
              n_slot <= cap_decode;
     }
   }
-  if (threadIdx.x == 0 && cap_decode > 0)
-    decode_work[0] = fits ? make_int4(nb, n_seg, n_slot, 0) : make_int4(0, 0, 0, 0);
+  // header: {nb, segments, partial slots, 0}; a step with decode pages that does not fit reports what it
+  // needed instead, {0, records, merges, -1}, and gets no decode work; a step without decode pages {0, 0, 0, 0}
+  if (threadIdx.x == 0 && cap_decode > 0) {
+    if (fits)
+      decode_work[0] = make_int4(nb, n_seg, n_slot, 0);
+    else if (nb > 0)
+      decode_work[0] = make_int4(0, 1 + nb + 2 * n_seg, n_merge, -1);
+    else
+      decode_work[0] = make_int4(0, 0, 0, 0);
+  }
 
   // prefill items, longest first
   for (int base = 0; base < num_seqs; base += kPlanThreads) {

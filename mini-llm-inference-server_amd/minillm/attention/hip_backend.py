@@ -30,30 +30,64 @@ from .. import _native
 from .base import AttentionBackend
 from .metadata import decode_plan_size
 
-def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool) -> tuple[int, int]:
-    """(resident wavefronts of the decode kernel on the chip, wavefronts one bin takes): 256 CUs x 4 SIMDs
-    x 3 per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two KV
-    heads when they pair up (decode_kernel_name), else one per KV head."""
+FULL_CHIP_CUS = 256  # MI355X: 8 XCDs x 32 CUs
+_CUS: dict = {}
+
+
+def device_cus(device=None) -> int:
+    """Compute units of the device the kernels run on (torch's multi_processor_count, read once per device):
+    a partitioned or smaller device holds fewer resident wavefronts, so the decode bins grow to match."""
+    if device is None or not torch.cuda.is_available():
+        return FULL_CHIP_CUS
+    index = torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    cus = _CUS.get(index)
+    if cus is None:
+        cus = _CUS[index] = int(torch.cuda.get_device_properties(index).multi_processor_count)
+    return cus
+
+
+def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int = FULL_CHIP_CUS) -> tuple[int, int]:
+    """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes): CUs x 4 SIMDs x 3
+    per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two KV heads
+    when they pair up (decode_kernel_name), else one per KV head."""
     if not kv_fp8:
-        return 256 * 4 * 3, num_kv_heads
+        return num_cus * 4 * 3, num_kv_heads
     if decode_kernel_name(True, num_heads, num_kv_heads) == "decode_pair_kernel":
-        return 256 * 4 * 2, num_kv_heads // 2
-    return 256 * 4 * 2, num_kv_heads
+        return num_cus * 4 * 2, num_kv_heads // 2
+    return num_cus * 4 * 2, num_kv_heads
 
 
-def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None = None, kv_fp8: bool = False) -> int:
-    """Pages per decode bin: the step's bins make one round of the kernel's resident wavefronts, clamped to
-    [8, 128] pages (~89 pages on the 256-row decode workload with a bf16 pool, ~67 with an fp8 one).  More
-    rounds of smaller bins measured slower (60 and 45 pages on bf16 decode_256: +10% and +7%), and so do
-    bins that leave resident wavefronts idle (fp8 pool at 89 pages: +10%).  Below the clamp, small steps
-    gain nothing: decode + merge over 8 / 32 / 64 rows of U[128, 4096] tokens took 27 / 56 / 99 us with
-    this choice against 30 / 74 / 140 us at 4 pages and 63 / 125 / 219 us at 1 page; 4 rows take ~16.5
-    us at every size from 1 to 8 pages (launch latency)."""
+def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None = None, kv_fp8: bool = False,
+                    num_cus: int = FULL_CHIP_CUS) -> int:
+    """Pages per decode bin: the step's bins make one round of the kernel's resident wavefronts on a device
+    of `num_cus` CUs, clamped to [8, 128] pages (~89 pages on the 256-row decode workload with a bf16 pool
+    on the full chip, ~67 with an fp8 one).  More rounds of smaller bins measured slower (60 and 45 pages
+    on bf16 decode_256: +10% and +7%), and so do bins that leave resident wavefronts idle (fp8 pool at 89
+    pages: +10%).  Below the clamp, small steps gain nothing: decode + merge over 8 / 32 / 64 rows of
+    U[128, 4096] tokens took 27 / 56 / 99 us with this choice against 30 / 74 / 140 us at 4 pages and
+    63 / 125 / 219 us at 1 page; 4 rows take ~16.5 us at every size from 1 to 8 pages (launch latency)."""
     forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
     if forced:
         return max(1, min(128, int(forced)))
-    slots, per_bin = decode_waves(num_heads or 4 * num_kv_heads, num_kv_heads, kv_fp8)
+    slots, per_bin = decode_waves(num_heads or 4 * num_kv_heads, num_kv_heads, kv_fp8, num_cus)
     return max(8, min(128, math.ceil(decode_pages * per_bin / slots)))
+
+
+class PlanOverflowError(RuntimeError):
+    """A decode plan did not fit the capacities it was given (its header reads {0, records, merges, -1})."""
+
+
+def check_plan_header(decode_work: torch.Tensor) -> None:
+    """Reads a decode plan's header back (one host synchronisation) and raises PlanOverflowError when the
+    step did not fit: the plan then holds no decode work, and the decode rows' outputs would stay unwritten."""
+    if decode_work.numel() < 4:
+        return
+    nb, records, merges, flag = decode_work[:4].tolist()
+    if flag == -1:
+        raise PlanOverflowError(f"decode plan overflow: the step needs {records} records and {merges} merges, "
+                                f"more than the capacities the plan was given")
 
 
 @dataclass
@@ -111,6 +145,9 @@ class HipBackend(AttentionBackend):
     # workgroups (a whole CU each) find no room beside it.  On mixed_128, one box: 410.8 us one after the
     # other, 412.8 us overlapped with decode enqueued first, 413.5 us with prefill first.
     overlap_mixed = False
+    # When set, every plan build reads the plan's header back (one host synchronisation) and raises
+    # PlanOverflowError if the decode plan did not fit its capacities; for tests and debugging.
+    check_plan = os.environ.get("MLLM_CHECK_PLAN", "") not in ("", "0")
 
     def __init__(self) -> None:
         self._lib = _native.lib()
@@ -288,7 +325,7 @@ class HipBackend(AttentionBackend):
         # a graph-captured step (StaticDecodeMetadata) stages its split size on the device; the
         # capacities then cover the smallest split it may stage
         split_dev = getattr(meta, "split_dev", None)
-        c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv, h, kv_fp8)
+        c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv, h, kv_fp8, device_cus(dev))
         g = h // hkv
         q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
         decode_rows = sum(1 for nn in news if nn == 1)
@@ -312,6 +349,8 @@ class HipBackend(AttentionBackend):
         self._plan = StepPlan(c, q_tile, n_dec, n_merge, n_pf, dec, mrg, pf, ws, meta_ptrs,
                               (*meta_ptrs, _ptr(dec), n_dec, _ptr(mrg), n_merge, c))
         self._planned, self._planned_fp8 = meta, kv_fp8
+        if self.check_plan and n_dec and not torch.cuda.is_current_stream_capturing():
+            check_plan_header(dec)
 
     def _workspace_for(self, nbytes: int, dev) -> torch.Tensor | None:
         if nbytes == 0:

@@ -28,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from ..attention.hip_backend import pages_per_split
+from ..attention.hip_backend import device_cus, pages_per_split
 from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata, decode_plan_size
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
@@ -113,7 +113,8 @@ class DecodeGraphs:
 
     def _split(self, pages: int) -> int:
         """The split size an eager step over `pages` decode pages uses with this pool."""
-        return pages_per_split(pages, self.num_kv_heads, self.num_heads, self.cache.quantized)
+        return pages_per_split(pages, self.num_kv_heads, self.num_heads, self.cache.quantized,
+                               device_cus(self.device))
 
     def _stage(self, c: _Captured, keys, seqs: list[SeqStep], token_ids: list[int]) -> None:
         bs = self.block_size

@@ -28,5 +28,7 @@ def hip():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
     from minillm import _native
+    from minillm.attention.hip_backend import HipBackend
 
+    HipBackend.check_plan = True  # every plan a GPU test builds through the backend must fit its capacities
     return _native.lib()

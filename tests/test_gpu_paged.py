@@ -503,6 +503,45 @@ def test_decode_rows_with_pages_past_their_last_token(hip, pages_per_split):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
+def test_plan_overflow_is_reported(hip):
+    # a decode plan sized one record (or one merge) short of what the step needs gets no decode work at all,
+    # and its header reports {0, records needed, merges needed, -1}, which check_plan_header turns into an
+    # error; at the exact size it fits and the header is {bins, segments, slots, 0}
+    from minillm import _native
+    from minillm.attention.hip_backend import PlanOverflowError, _ptr, check_plan_header
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    rng = random.Random(5)
+    steps = [(rng.randrange(0, 300), 1) for _ in range(40)]
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=400, seed=5)
+    meta = AttentionMetadata.build([SeqStep(c, n, list(b)) for c, n, b in wl.seqs], wl.block_size, DEV)
+    split = 8
+    rows, kv0 = [], 0
+    for i, (c, n) in enumerate(steps):
+        pages = -(-(c + n) // 16)
+        rows.append((i, pages, kv0, i, c + n))
+        kv0 += pages
+    bins, segs, merges, slots = decode_plan.restate(rows, split)
+    need, need_m = 1 + len(bins) + 2 * len(segs), len(merges)
+    assert need_m > 1
+    lib = _native.lib()
+    st = _native.stream_ptr(DEV)
+    for cap, cap_m, fits in ((need, need_m, True), (need - 1, need_m, False), (need, need_m - 1, False)):
+        dec = torch.full((4 * cap,), -1, dtype=torch.int32, device=DEV)
+        mrg = torch.full((4 * cap_m,), -1, dtype=torch.int32, device=DEV)
+        lib.call("mllm_plan", meta.qo_indptr.data_ptr(), meta.kv_indptr.data_ptr(), meta.seq_lens_i32.data_ptr(),
+                 len(steps), split, 64, dec.data_ptr(), cap, _ptr(mrg), cap_m, 0, 0, st)
+        torch.cuda.synchronize()
+        if fits:
+            assert dec[:4].tolist() == [len(bins), len(segs), slots, 0]
+            check_plan_header(dec)
+        else:
+            assert dec[:4].tolist() == [0, need, need_m, -1]
+            assert (dec[4:] == -1).all() and (mrg == -1).all()  # no decode work written
+            with pytest.raises(PlanOverflowError, match=f"{need} records and {need_m} merges"):
+                check_plan_header(dec)
+
+
 def test_prefill_item_without_visible_keys_writes_nothing(hip):
     # a plan record whose row has no visible key (kv_end 0: seq_lens below the new-token count, which the
     # metadata build never produces) makes the workgroup return before any load; out keeps its sentinel

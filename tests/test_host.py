@@ -105,6 +105,29 @@ def test_split_size_heuristic(monkeypatch):
     assert hip_backend.pages_per_split(34000, 8) == 5
 
 
+def test_split_size_follows_the_device_cu_count(monkeypatch):
+    # bins are one round of the kernel's resident wavefronts: a device with a quarter of the CUs gets bins
+    # four times as long (up to the 128-page clamp); the CU count comes from torch's device properties
+    import math
+    from types import SimpleNamespace
+
+    from minillm.attention import hip_backend
+
+    monkeypatch.delenv("MLLM_PAGES_PER_SPLIT", raising=False)
+    monkeypatch.setattr(hip_backend, "_CUS", {})
+    monkeypatch.setattr(hip_backend.torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(hip_backend.torch.cuda, "get_device_properties",
+                        lambda index: SimpleNamespace(multi_processor_count=64 if index == 1 else 256))
+    assert hip_backend.device_cus("cuda:1") == 64 and hip_backend.device_cus("cuda:0") == 256
+    assert hip_backend.device_cus(None) == hip_backend.FULL_CHIP_CUS
+    full = hip_backend.pages_per_split(10000, 8, 32, False, hip_backend.device_cus("cuda:0"))
+    part = hip_backend.pages_per_split(10000, 8, 32, False, hip_backend.device_cus("cuda:1"))
+    assert full == hip_backend.pages_per_split(10000, 8) == math.ceil(10000 * 8 / (256 * 12)) == 27
+    assert part == math.ceil(10000 * 8 / (64 * 12)) == 105
+    assert hip_backend.pages_per_split(10000, 8, 32, True, 64) == math.ceil(10000 * 4 / (64 * 8)) == 79
+    assert hip_backend.pages_per_split(40000, 8, 32, False, 64) == 128  # clamped
+
+
 def test_workloads_are_deterministic_and_sized():
     from minillm import workloads
 
