@@ -11,7 +11,9 @@ same shapes, so that its rounding is the reference's own:
   a bottom-right aligned `tril(length - n)` mask otherwise (`paged_torch_ref.py:61-73`).
 
 Runs on any torch device.  On a GPU, callers pass float32 tensors (the bf16 batched-matmul path of
-torch is avoided there); on the CPU it runs in the caller's dtype, exactly as the reference does.
+torch is avoided there), or bf16 tensors with `fused=True`, which pins SDPA to torch's fused
+memory-efficient kernel (the reference's torch_ref arithmetic in bf16 on a GPU); on the CPU it runs in
+the caller's dtype, exactly as the reference does.
 
 fp8 pools (torch.float8_e4m3fn, the reference's planned fp8 KV cache: docs/distributed_inference_plan.md:310)
 hold e4m3fn(x * (1 / scale)) with one scale per tensor: `write_kv` quantizes with torch's own cast and
@@ -116,12 +118,24 @@ def gather(cache: torch.Tensor, block_tables: torch.Tensor, length: int) -> torc
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Tensor | None = None,
-         is_causal: bool = False, p_round: torch.dtype | None = None) -> torch.Tensor:
+         is_causal: bool = False, p_round: torch.dtype | None = None, fused: bool = False) -> torch.Tensor:
     """`F.scaled_dot_product_attention(..., enable_gqa=True)` (scale 1/sqrt(Dh), bottom-right causal
     when `is_causal`: the reference only sets it when Tq == Tk).  With `p_round`, the same mathematics
     written out in q's dtype, with the softmax probabilities rounded to `p_round` before the product with
     V, which is how flash-style bf16 kernels form P.  That variant is not the reference's computation:
-    it is the noise-floor reference of bf16 attention arithmetic for end-to-end comparisons."""
+    it is the noise-floor reference of bf16 attention arithmetic for end-to-end comparisons.
+
+    With `fused` (GPU tensors), the library SDPA pinned to torch's fused memory-efficient kernel, with
+    K/V expanded to one head per query head (that kernel takes no grouped heads; each query head still
+    reads its own KV head's values): the reference's torch_ref arithmetic on a GPU in bf16, without the
+    math path, whose bf16 batched products are not used here."""
+    if fused:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        g = q.shape[1] // k.shape[1]
+        k, v = k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1)
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal)
     if p_round is None:
         return F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal, enable_gqa=True)
     g = q.shape[1] // k.shape[1]
@@ -138,12 +152,13 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Ten
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
                     compute_dtype: torch.dtype | None = None, k_scale: float = 1.0,
-                    v_scale: float = 1.0, p_round: torch.dtype | None = None) -> torch.Tensor:
+                    v_scale: float = 1.0, p_round: torch.dtype | None = None, fused: bool = False) -> torch.Tensor:
     """Reference `paged_torch_ref.py:40-74`.  q [N, H, Dh] -> [N, H, Dh]; the step's own k/v must
     already be in the pool.  Scale 1/sqrt(Dh); GQA through `enable_gqa`.  With `compute_dtype` the
     gathered context and q are converted to it before SDPA (and the result back to q's dtype): how the
     oracle runs on a GPU, in float32.  An fp8 pool's gathered rows are dequantized (value * scale, in
-    `compute_dtype` or q's dtype).  `p_round` selects the rounded-P variant of `sdpa`."""
+    `compute_dtype` or q's dtype).  `p_round` selects the rounded-P variant of `sdpa`, `fused` its
+    fused-kernel variant."""
     if getattr(k_cache, "dtype", None) == FP8:
         cd = compute_dtype or q.dtype
 
@@ -152,7 +167,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
 
         kb, vb = k_cache.view(torch.uint8), v_cache.view(torch.uint8)  # gathered as bytes (no float8 indexing)
         out = paged_attention(q.to(cd), _Converted(kb, deq(k_scale)), _Converted(vb, deq(v_scale)), meta,
-                              p_round=p_round)
+                              p_round=p_round, fused=fused)
         return out.to(q.dtype)
     if compute_dtype is not None and compute_dtype != q.dtype:
         orig = q.dtype
@@ -160,7 +175,8 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         def conv(t):
             return t.to(compute_dtype)
 
-        out = paged_attention(conv(q), _Converted(k_cache, conv), _Converted(v_cache, conv), meta, p_round=p_round)
+        out = paged_attention(conv(q), _Converted(k_cache, conv), _Converted(v_cache, conv), meta, p_round=p_round,
+                              fused=fused)
         return out.to(orig)
     out = torch.empty_like(q)
     starts, lens, news = meta.query_start_loc, meta.seq_lens, meta.num_new
@@ -177,7 +193,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         if any(lens[i] != longest for i in decode):
             ends = torch.tensor([lens[i] for i in decode], device=q.device)
             mask = (torch.arange(longest, device=q.device)[None, :] < ends[:, None])[:, None, None, :]
-        out[token_idx] = sdpa(qd, k, v, attn_mask=mask, p_round=p_round)[:, :, 0]
+        out[token_idx] = sdpa(qd, k, v, attn_mask=mask, p_round=p_round, fused=fused)[:, :, 0]
 
     for i, n in enumerate(news):
         if n == 1:
@@ -187,10 +203,10 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         v = gather(v_cache, meta.block_tables[i:i + 1], length)
         qi = q[s:s + n].transpose(0, 1)[None]
         if n == length:
-            o = sdpa(qi, k, v, is_causal=True, p_round=p_round)
+            o = sdpa(qi, k, v, is_causal=True, p_round=p_round, fused=fused)
         else:
             mask = torch.ones(n, length, dtype=torch.bool, device=q.device).tril(diagonal=length - n)
-            o = sdpa(qi, k, v, attn_mask=mask, p_round=p_round)
+            o = sdpa(qi, k, v, attn_mask=mask, p_round=p_round, fused=fused)
         out[s:s + n] = o[0].transpose(0, 1)
     return out
 

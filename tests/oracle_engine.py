@@ -23,18 +23,21 @@ def oracle_metadata(seqs, block_size, device):
 class OracleBackend:
     """write_kv + gather/SDPA restated from the reference; attention computed in float32.  With
     `p_round` (torch.bfloat16) the softmax probabilities are rounded before the product with V: bf16
-    attention arithmetic, the noise-floor reference of end-to-end comparisons."""
+    attention arithmetic, the noise-floor reference of end-to-end comparisons.  With `fused` and
+    compute_dtype torch.bfloat16, SDPA runs in bf16 on torch's fused memory-efficient kernel: the
+    reference's torch_ref backend as it computes on a GPU in bf16."""
 
     name = "oracle"
 
-    def __init__(self, compute_dtype=torch.float32, p_round=None) -> None:
+    def __init__(self, compute_dtype=torch.float32, p_round=None, fused: bool = False) -> None:
         self.compute_dtype = compute_dtype
         self.p_round = p_round
+        self.fused = fused
 
     def forward(self, q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
         torch_ref.write_kv(k_cache, v_cache, meta.slot_mapping, k, v, k_scale, v_scale)
         return torch_ref.paged_attention(q, k_cache, v_cache, meta, compute_dtype=self.compute_dtype,
-                                         k_scale=k_scale, v_scale=v_scale, p_round=self.p_round)
+                                         k_scale=k_scale, v_scale=v_scale, p_round=self.p_round, fused=self.fused)
 
     def prefill(self, q, k, v, key_valid=None, **kwargs):
         dt = q.dtype

@@ -13,13 +13,23 @@ continuous batching, prefill-first, no prefix caching.  The full 128 x 256 = 32,
    over the same tokens, so every position has logits from both.  Drift(oracle, HIP): mean KL(oracle ||
    HIP), max |dlogit|, and top-1 flips where the oracle's top-1/top-2 margin exceeds 0.5 logit.
 3. The noise floor: the oracle engine again, with its softmax probabilities rounded to bf16 before the
-   product with V (bf16 attention arithmetic), forced to the same tokens, against step 2's logits.
-4. The HIP engine with its decode steps replayed as captured HIP graphs, forced to the same tokens,
+   product with V (bf16 attention arithmetic), forced to the same tokens, against step 2's logits; the
+   HIP engine's drift from this run is logged as well.
+4. The reference's torch_ref backend as it runs on a GPU in bf16 (reference tests/test_kernels.py:75-112
+   compares kernels with it there): the oracle engine with bf16 tensors and SDPA on torch's fused
+   memory-efficient kernel, forced to the same tokens.  Logged: the HIP engine's drift from it, which
+   counts the positions where the HIP engine's greedy token differs from that run's argmax over the same
+   prefix (teacher-forced greedy identity), and its own drift from step 2.
+5. The HIP engine with its decode steps replayed as captured HIP graphs, forced to the same tokens,
    against step 2's logits.
-Pass, for steps 1 and 4: no clear-margin flip, and mean KL and max |dlogit| within 2x the noise floor's
-(with the reference's floors 1e-5 and 0.125, correctness.py:25-28).  The greedy comparison is logged
-too: positions where the HIP engine's greedy token is not the oracle's argmax, and the largest oracle
-margin among them.
+Pass, for steps 1 and 5: no clear-margin flip, and mean KL and max |dlogit| within 2x the noise floor's
+(the reference's floors 1e-5 and 0.125, correctness.py:25-28, apply below that).  This limit is this
+build's calibration for a kernel backend, which docs/decisions/04-correctness.md:29 leaves to each
+backend; the reference's own kernel test calibrates with drift(ref, ref) and so applies the floors
+alone (tests/test_kernels.py:112), which bf16 attention arithmetic does not meet against a float32
+oracle.  Also required: no clear-margin flip against the bf16-P run or the bf16 torch_ref run.  The
+greedy comparison is logged for every pair: positions where the argmaxes differ, and the largest
+reference-side margin among them.
 """
 
 import sys
@@ -112,7 +122,7 @@ def run_engine(model, backend, builder, prompts, blocks, sampler, label, **kw):
     while core.has_work():
         for o in core.step().outputs:
             out.setdefault(o.req_id, []).extend(o.new_token_ids)
-        if len(core.step_log) % 32 == 0:
+        if len(core.step_log) % 64 == 0:
             progress(f"{label}: step {len(core.step_log)}, {time.perf_counter() - t0:.0f} s")
     st = core.stats()
     info = {"steps": len(core.step_log), "seconds": round(time.perf_counter() - t0, 1),
@@ -149,41 +159,61 @@ def test_engine_8b_teacher_forced_against_oracle(hip, llama8b, capsys):
     tokens, hip_info = run_engine(model, get_backend("hip"), None, prompts, blocks, greedy_kept, "hip greedy")
     assert all(len(tokens[f"r{i}"]) == STEPS for i in range(REQUESTS))
 
-    def forced(store=None, drift=None, against=None):
+    def forced(*pairs, store=None):
+        """A sampler forced to the HIP engine's tokens.  Each pair (drift, other logits, run_is_ref) adds this
+        run's logits against the other run's at the same positions, this run as the reference side when
+        run_is_ref."""
         def sample(reqs, logits):
             idx, pos = _rows(reqs)
             if store is not None:
                 store[idx, pos] = logits
-            if drift is not None:
-                ref, tst = (logits, against[idx, pos]) if store is not None else (against[idx, pos], logits)
-                drift.add(ref, tst)
+            for drift, other, run_is_ref in pairs:
+                o = other[idx, pos]
+                if run_is_ref:
+                    drift.add(logits, o)
+                else:
+                    drift.add(o, logits)
             return [tokens[r.req_id][len(r.output)] for r in reqs]
         return sample
 
     # 2. the oracle engine forced to those tokens: the reference logits, and the HIP engine's drift from them
     ours = Drift()
     _, oracle_info = run_engine(model, OracleBackend(), oracle_metadata, prompts, blocks,
-                                forced(store=ref_logits, drift=ours, against=hip_logits), "oracle fp32")
-    # 3. the noise floor: bf16 attention arithmetic in the oracle
-    noise = Drift()
+                                forced((ours, hip_logits, True), store=ref_logits), "oracle fp32")
+    # 3. the noise floor: bf16 attention arithmetic in the oracle (P rounded to bf16); HIP against it too
+    noise, hip_vs_p = Drift(), Drift()
     _, noise_info = run_engine(model, OracleBackend(p_round=torch.bfloat16), oracle_metadata, prompts, blocks,
-                               forced(drift=noise, against=ref_logits), "oracle bf16-P")
-    # 4. the HIP engine with decode steps as captured HIP graphs
+                               forced((noise, ref_logits, False), (hip_vs_p, hip_logits, True)), "oracle bf16-P")
+    # 4. the reference's torch_ref arithmetic on the GPU: SDPA in bf16 (torch's fused kernel); HIP against it,
+    #    and it against the float32 oracle
+    hip_vs_bf16, bf16_vs_fp32 = Drift(), Drift()
+    _, bf16_info = run_engine(model, OracleBackend(compute_dtype=torch.bfloat16, fused=True), oracle_metadata,
+                              prompts, blocks, forced((hip_vs_bf16, hip_logits, True), (bf16_vs_fp32, ref_logits, False)),
+                              "oracle bf16 sdpa")
+    # 5. the HIP engine with decode steps as captured HIP graphs
     graphs = Drift()
     _, graph_info = run_engine(model, get_backend("hip"), None, prompts, blocks,
-                               forced(drift=graphs, against=ref_logits), "hip graphs", decode_graphs=True)
+                               forced((graphs, ref_logits, False)), "hip graphs", decode_graphs=True)
 
     n, o, g = noise.summary(), ours.summary(), graphs.summary()
     kl_limit = 2 * max(n["mean_kl"], KL_FLOOR)
     diff_limit = 2 * max(n["max_abs_diff"], DIFF_FLOOR)
-    progress(f"runs: hip {hip_info}, oracle {oracle_info}, noise {noise_info}, graphs {graph_info}")
-    progress(f"noise floor (oracle bf16-P vs fp32): {n}")
-    progress(f"hip eager vs oracle: {o}")
-    progress(f"hip graphs vs oracle: {g}")
-    progress(f"limits: mean KL <= {kl_limit:.3e}, max |dlogit| <= {diff_limit:.4f}")
+    progress(f"runs (s): hip {hip_info['seconds']}, oracle fp32 {oracle_info['seconds']}, bf16-P {noise_info['seconds']}, "
+             f"bf16 sdpa {bf16_info['seconds']}, graphs {graph_info['seconds']} ({graph_info['graph_replays']} replays)")
+    for label, d in (("noise floor: oracle bf16-P vs oracle fp32", n), ("hip eager vs oracle fp32", o),
+                     ("hip graphs vs oracle fp32", g), ("hip eager vs oracle bf16-P", hip_vs_p.summary()),
+                     ("hip eager vs torch_ref bf16 sdpa (greedy identity)", hip_vs_bf16.summary()),
+                     ("torch_ref bf16 sdpa vs oracle fp32", bf16_vs_fp32.summary())):
+        progress(f"{label}: KL {d['mean_kl']:.3e} max|dlogit| {d['max_abs_diff']:.4f} flips>{MARGIN} "
+                 f"{d['clear_margin_flips']} argmax differs {d['argmax_differs']}/{d['positions']} "
+                 f"(max margin there {d['max_margin_where_differs']:.4f})")
+    progress(f"limits (2x the noise floor): mean KL <= {kl_limit:.3e}, max |dlogit| <= {diff_limit:.4f}")
     assert o["positions"] == n["positions"] == g["positions"] == REQUESTS * STEPS
+    assert hip_vs_bf16.positions == hip_vs_p.positions == REQUESTS * STEPS
     assert graph_info["graph_replays"] > 0
     for name, d in (("eager", o), ("graphs", g)):
         assert d["clear_margin_flips"] == 0, f"{name}: top-1 differs where the oracle leads by > {MARGIN}: {d}"
         assert d["mean_kl"] <= kl_limit, f"{name}: mean KL {d['mean_kl']:.3e} > {kl_limit:.3e}"
         assert d["max_abs_diff"] <= diff_limit, f"{name}: max |dlogit| {d['max_abs_diff']:.4f} > {diff_limit:.4f}"
+    for name, d in (("bf16-P", hip_vs_p.summary()), ("bf16 sdpa", hip_vs_bf16.summary())):
+        assert d["clear_margin_flips"] == 0, f"vs {name}: top-1 differs where it leads by > {MARGIN}: {d}"
