@@ -4,8 +4,8 @@
 Headline workload (decode_256): one layer of a ragged decode step of Llama-3.1-8B's attention shape
 (32 query / 8 KV heads, head_dim 128, 16-token blocks, bf16) over 256 rows whose cached contexts are
 uniform in [128, 4096], one new token each, pool = 2x the pages with a shuffled assignment.  A step
-is KV append + split-KV paged decode + split merge, with the step's metadata and work plan built
-beforehand (they are built once per engine step and shared by all 32 layers; their cost is reported
+is KV append + split-KV paged decode + split merge, issued by one host call per layer
+(mllm_attention_forward), with the step's metadata and work plan built beforehand (they are built once per engine step and shared by all 32 layers; their cost is reported
 separately, as a median after a warm-up).  `value` is decode tokens/s of the 32-layer model:
 256 / (32 x layer time).
 
@@ -17,7 +17,7 @@ SDPA; bf16) over all 256 rows on this host's cores (torch.set_num_threads(os.cpu
 workloads on the GPU with their own kernels' rates and the same CPU baseline:
   decode_4    4 rows (contexts 37/128/211/500 + 1): step and decode-launch time (latency-bound);
   mixed_128   8 prefill + 120 decode rows: prefill launch TFLOP/s and fraction of the bf16 peak over
-              its own launch, decode launch GB/s, and the backend's own step (backend_step_us);
+              its own launch, decode launch GB/s, and the step (append, decode + merge, prefill);
   prefix_64   64 rows over a shared 2,048-token prefix: prefill launch TFLOP/s and fraction;
   decode_256_fp8  the headline step on an fp8 (e4m3fn) pool: decode launch GB/s and fraction;
   gemm_8192   torch.mm (hipBLASLt) on 8192^3 bf16 operands, random and zero: the MFMA rate this GPU
@@ -390,11 +390,12 @@ def shared_step_costs(wl, backend, dev, reps: int = 10):
 
 
 def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
-    """One layer's step on the GPU: KV append, decode + merge, prefill, launched one after another on
-    the current stream; `warmup` untimed steps, then `steps` timed ones between two synchronisations,
-    then the same `steps` again with HIP events on that stream around every decode and prefill launch
-    (the kernels' own durations; the events stay out of the timed steps).  Mixed workloads also time the
-    backend's own step (`attend`)."""
+    """One layer's step on the GPU: KV append, decode + merge and prefill in one host call
+    (HipBackend.run_layer, mllm_attention_forward) on the current stream; `warmup` untimed steps, then
+    `steps` timed ones between two synchronisations, then the same `steps` again as separate calls with
+    HIP events on that stream around every decode and prefill launch (the kernels' own durations; the
+    events stay out of the timed steps).  Also times the public `forward` (argument checks and the output
+    allocation included) over the same steps."""
     import torch
 
     from minillm.attention.metadata import AttentionMetadata, SeqStep
@@ -409,58 +410,44 @@ def measure_layer(wl, backend, dev, steps: int, warmup: int, fp8: bool):
     plan = backend.plan(meta, wl.h, wl.hkv, wl.dh, dev, fp8)
     out = torch.empty_like(q)
 
-    def step(ev=None):
+    def step():
+        backend.run_layer(q, k, v, pool_k, pool_v, meta, out, k_scale=ks, v_scale=vs)
+
+    def step_events(ev):
         backend.append(k, v, pool_k, pool_v, meta, ks, vs)
         if plan.num_decode:
-            if ev is not None:
-                ev[0].record()
+            ev[0].record()
             backend.run_decode(q, pool_k, pool_v, meta, out, ks, vs)
-            if ev is not None:
-                ev[1].record()
+            ev[1].record()
             backend.run_merge(q, meta, out)
         if plan.num_prefill:
-            if ev is not None:
-                ev[2].record()
+            ev[2].record()
             backend.run_prefill(q, pool_k, pool_v, meta, out, ks, vs)
-            if ev is not None:
-                ev[3].record()
+            ev[3].record()
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):  # no events between the launches
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps, (time.perf_counter() - w0) * 1e3
+
+    step_ms, wall_ms = timed(step)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(steps):  # the same steps as separate calls, with HIP events around each launch
+        step_events(evs[i])
     torch.cuda.synchronize()
-    w0 = time.perf_counter()
-    start.record()
-    for _ in range(steps):  # the timed steps: no events between their launches
-        step()
-    stop.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - w0) * 1e3
-    for i in range(steps):  # the same steps again, with HIP events around each launch: the kernels' own time
-        step(evs[i])
-    torch.cuda.synchronize()
-    res = {"wall_ms": wall_ms, "step_ms": start.elapsed_time(stop) / steps,
-           "dec_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0,
-           "pf_ms": statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0,
-           "plan": plan, "meta": meta, "tensors": (q, k, v, pool_k, pool_v)}
-    if plan.num_decode and plan.num_prefill:  # the backend's own mixed step (attend), no events inside
-        def ostep():
-            backend.append(k, v, pool_k, pool_v, meta, ks, vs)
-            backend.attend(q, pool_k, pool_v, meta, out, ks, vs)
-
-        for _ in range(max(3, warmup)):
-            ostep()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(steps):
-            ostep()
-        b.record()
-        torch.cuda.synchronize()
-        res["backend_step_ms"] = a.elapsed_time(b) / steps
-    return res
+    forward_ms, _ = timed(lambda: backend.forward(q, k, v, pool_k, pool_v, meta, ks, vs))
+    return {"wall_ms": wall_ms, "step_ms": step_ms, "forward_ms": forward_ms,
+            "dec_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs) if plan.num_decode else 0.0,
+            "pf_ms": statistics.mean(e[2].elapsed_time(e[3]) for e in evs) if plan.num_prefill else 0.0,
+            "plan": plan, "meta": meta, "tensors": (q, k, v, pool_k, pool_v)}
 
 
 def kernel_rates(wl, r, kv_elem: int) -> dict:
@@ -474,9 +461,7 @@ def kernel_rates(wl, r, kv_elem: int) -> dict:
         tf = wl.prefill_flops() / (r["pf_ms"] * 1e-3) / 1e12
         out.update(prefill_us=round(r["pf_ms"] * 1e3, 2), prefill_flops=wl.prefill_flops(),
                    prefill_tflops=round(tf, 1), prefill_frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
-    if "backend_step_ms" in r:
-        out["backend_step_us"] = round(r["backend_step_ms"] * 1e3, 2)
-        out["backend_tokens_per_s_32_layers"] = round(wl.num_tokens / (LAYERS * r["backend_step_ms"] * 1e-3), 1)
+    out["forward_us"] = round(r["forward_ms"] * 1e3, 2)  # the public forward: checks + allocation + the call
     return out
 
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define MLLM_ABI_VERSION 3
+#define MLLM_ABI_VERSION 4
 
 #define MLLM_OK 0
 #define MLLM_ERR_INVALID (-1)
@@ -149,7 +149,7 @@ int mllm_rope_kv_append(const void* q, int64_t q_stride_tok, int64_t q_stride_he
  * num_merge_work merges gets no decode work at all: the header then reads {0, records needed, merges
  * needed, -1} (a step with no decode pages reads {0, 0, 0, 0}), so the decode and merge kernels never
  * index past a workspace sized for num_decode_work partial slots, and a caller that reads the header
- * sees the overflow.  Prefill items past num_prefill_work are dropped.  pages_per_split <= 128.
+ * sees the overflow.  Prefill items past num_prefill_work are dropped.  pages_per_split <= 192.
  */
 int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_seqs,
               int32_t pages_per_split, int32_t q_tile_tokens, int32_t* decode_work, int32_t num_decode_work,
@@ -158,7 +158,7 @@ int mllm_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t*
 
 /*
  * mllm_plan with the split size read from device memory at run time (*pages_per_split, clamped to
- * [min_pages_per_split, 128]).  No counterpart in the reference: it serves HIP-graph capture of decode steps
+ * [min_pages_per_split, 192]).  No counterpart in the reference: it serves HIP-graph capture of decode steps
  * (the reference's planned M8, docs/distributed_inference_plan.md:309), where one captured plan launch
  * re-plans every replayed step.  The caller checks on the host that a staged step's items fit the
  * capacities at the split size it stages (or runs that step without the graph), so no item is dropped;
@@ -169,8 +169,9 @@ int mllm_plan_dev(const int32_t* qo_indptr, const int32_t* kv_indptr, const int3
                   int32_t* decode_work, int32_t num_decode_work, int32_t* merge_work, int32_t num_merge_work,
                   int32_t* prefill_work, int32_t num_prefill_work, void* stream);
 
-/* Bytes of fp32 split-KV partials for num_decode_work partial slots (a plan of num_decode_work records
- * has fewer slots than records). */
+/* Bytes of the fp32 split-KV partials a plan of num_decode_work records can need: (num_decode_work - 1) / 2
+ * partial slots (every slot is a segment of a cut row, and each segment takes two records after the
+ * header), each (m, l, acc[Dh]) for num_heads heads. */
 int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim);
 
 /*
@@ -211,7 +212,7 @@ int mllm_merge_splits(const int32_t* merge_work, int32_t num_merge_work, int32_t
  * device array of this library instead of a caller workspace: each GPU the library runs on holds its
  * own copy until the process ends, looked up on the first call on that device (the current device;
  * the stream must belong to it).  A step whose partials need more
- * (mllm_decode_workspace_bytes(num_decode_work, H, Dh) > 64 MiB when num_merge_work > 0; 4,032 plan
+ * (mllm_decode_workspace_bytes(num_decode_work, H, Dh) > 64 MiB when num_merge_work > 0; 8,066 plan
  * records at H = 32, Dh = 128) is rejected with MLLM_ERR_INVALID.  Calls that overlap on one GPU (other streams or
  * threads) share the array and race; calls in order on one stream do not.  Arguments and results are
  * mllm_paged_decode's and mllm_merge_splits' (16-bit pools), bit for bit.
@@ -239,6 +240,51 @@ int mllm_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
                        const int32_t* kv_indices, const int32_t* seq_lens, const int32_t* prefill_work,
                        int32_t num_prefill_work, int32_t q_tile_tokens, float softmax_scale, int32_t dtype,
                        void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+
+/*
+ * The step-constant arguments of mllm_attention_forward: shapes, the step's metadata (AttentionMetadata's
+ * device fields), its work plan (mllm_plan) and the decode workspace.  The caller fills one per step and
+ * passes its address to every layer's call; the library reads it during each call only.
+ */
+typedef struct mllm_layer_step {
+  int64_t num_blocks;          /* blocks of each pool */
+  int64_t num_tokens;          /* N: new tokens of the step (rows of q, k, v, out) */
+  const int64_t* slot_mapping; /* [N] */
+  const int32_t* qo_indptr;    /* [S + 1] */
+  const int32_t* kv_indptr;    /* [S + 1] */
+  const int32_t* kv_indices;
+  const int32_t* seq_lens;     /* [S], int32 */
+  const int32_t* decode_work;  /* the plan's three lists and their capacities */
+  const int32_t* merge_work;
+  const int32_t* prefill_work;
+  void* workspace;             /* decode partials, >= mllm_decode_workspace_bytes(num_decode_work, H, Dh)
+                                  when num_merge_work > 0 */
+  int64_t workspace_bytes;
+  int32_t num_decode_work, num_merge_work, num_prefill_work;
+  int32_t pages_per_split, q_tile_tokens;
+  int32_t num_heads, num_kv_heads, head_dim, block_size;
+  int32_t dtype;               /* q, k, v, cos, sin, q_rot, out: MLLM_DTYPE_BF16 or MLLM_DTYPE_F16 */
+  int32_t kv_fp8;              /* 0: pools of `dtype`; 1: fp8 e4m3fn pools with k_scale / v_scale */
+  float softmax_scale;
+} mllm_layer_step;
+
+/*
+ * One layer's whole hot path in one call (reference TorchRefBackend.forward = write_kv + paged_attention,
+ * src/minillm/attention/torch_ref.py:46-48; the backend's forward, base.py:35-45): on `stream`, the KV
+ * append of k and v at slot_mapping (mllm_kv_append / _fp8), or with cos and sin given the model's RoPE
+ * of q and k fused into it (mllm_rope_kv_append / _fp8, the rotated q written to q_rot, which attention
+ * then reads); then the decode rows' split-KV attention and merge (mllm_paged_decode / _fp8 +
+ * mllm_merge_splits) and the multi-token rows' prefill (mllm_paged_prefill / _fp8), the same launches
+ * with the same results as those calls in that order.  q, k, v: [N, heads, Dh] with element strides
+ * (tok, head); cos / sin: [N, Dh] rows with stride cs_stride_tok, or NULL; q_rot (when cos is given) and
+ * out: contiguous [N, H, Dh].  k_scale / v_scale apply to fp8 pools and must be 1 otherwise.  One host
+ * call instead of three to four, for steps whose launches cost the host more than the GPU's work.
+ */
+int mllm_attention_forward(const mllm_layer_step* step, const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                           const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                           int64_t v_stride_tok, int64_t v_stride_head, const void* cos, const void* sin,
+                           int64_t cs_stride_tok, void* q_rot, void* k_cache, void* v_cache, float k_scale,
+                           float v_scale, void* out, void* stream);
 
 /*
  * Contiguous causal attention, the backend's `prefill` method (reference

@@ -37,10 +37,21 @@ namespace mllm {
 namespace {
 
 constexpr int kHeadDim = 128;
-#ifndef MLLM_DECODE_WAVES
-#define MLLM_DECODE_WAVES 4
-#endif
-constexpr int kWaves = MLLM_DECODE_WAVES;  // KV heads per workgroup
+constexpr int kWaves = 4;  // KV heads per workgroup of the decode kernel on small steps
+// Whole-page decode (16-bit pools): one workgroup of 8 wavefronts reads all 8 KV heads of a bin's pages,
+// each 16-token page of the pool one contiguous 32 KB run, at 2 wavefronts per SIMD: one workgroup per CU.
+// The library launches it when the KV heads are a multiple of 8 and the split size is at least
+// kWholePageMinSplit pages; the host then sizes the bins so the step is one round of workgroups (at most
+// one bin per CU).  Same box, against 4-wavefront workgroups at 3 per SIMD: decode_256 341.7 against
+// 349.6 us (255 bins of 134 pages against 383 of 89), mixed_128's decode 322.8 against 329.4 us, 128 rows
+// of 960 tokens 81.4 against 82.8 us; on small steps it is slower (4 rows: 16.0 against 11.5 us; 32 rows of
+// 960 tokens at 8 pages a bin: 27.8 against 26.7 us), hence the threshold.
+constexpr int kWavesWhole = 8;
+constexpr int kOccupancyWhole = 2;
+constexpr int kWholePageMinSplit = 24;
+__host__ __device__ constexpr bool whole_page(bool fp8, int num_kv_heads, int pages_per_split) {
+  return !fp8 && num_kv_heads % kWavesWhole == 0 && pages_per_split >= kWholePageMinSplit;
+}
 #ifndef MLLM_DECODE_LAZY_RESCALE
 #define MLLM_DECODE_LAZY_RESCALE 1
 #endif
@@ -115,14 +126,31 @@ struct LoadCursor {
   }
 };
 
+// A segment's page ids, one per lane in three registers: pages 0-63, 64-127 and 128-191 of the segment
+// (a bin holds at most kMaxSplitPages pages).
+constexpr int kMaxSplitPages = 192;
+struct PageIds {
+  int r[3];
+};
+__device__ __forceinline__ PageIds load_page_ids(const int32_t* kv_indices, const int4& r0, int lane) {
+  PageIds p;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) p.r[i] = lane + 64 * i < r0.y ? kv_indices[r0.x + 64 * i + lane] : 0;
+  return p;
+}
+// Page `page` (wave-uniform) of the segment.
+__device__ __forceinline__ int page_id(const PageIds& p, int page) {
+  return __builtin_amdgcn_readlane(page < 64 ? p.r[0] : (page < 128 ? p.r[1] : p.r[2]), page & 63);
+}
+
 // Loads the 16-token tile at `at` of this wave's page range (lane (c, g); kbase/vbase: this head's bytes
 // of the pools, strides in bytes).
 template <bool F8, bool NT>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, const char* kbase, const char* vbase, int64_t tok_stride,
-                                          int64_t blk_stride, int page_lo, int page_hi, LoadCursor at, int c, int g,
+                                          int64_t blk_stride, const PageIds& pages, LoadCursor at, int c, int g,
                                           TileRegs<F8>& r) {
   const int page = at.page, sub = at.sub;
-  int blk = __builtin_amdgcn_readlane(page < 64 ? page_lo : page_hi, page & 63);
+  int blk = page_id(pages, page);
   if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
   const int64_t off = (int64_t)blk * blk_stride + (int64_t)(sub * 16) * tok_stride;
   const char* kp = kbase + off + c * tok_stride;
@@ -229,15 +257,15 @@ __device__ __forceinline__ SegRec seg_rec(const int4* segs, int g) {
 // load of a segment's last tile fetches the next segment's first tile.  So the stream does not stop at
 // a row boundary: a new segment costs its finalisation (output or partial stores) and a fresh
 // online-softmax state.
-template <typename T, bool F8, bool NT, int OCC>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_kernel(
+template <typename T, bool F8, bool NT, int OCC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void decode_kernel(
     const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   // the KV-head group varies fastest, so the workgroups of one bin (adjacent heads of the same pages)
   // run side by side
   const int hg = blockIdx.x % a.HG;
   const int bin = blockIdx.x / a.HG;
-  const int kvh = hg * kWaves + (threadIdx.x >> 6);
+  const int kvh = hg * WAVES + (threadIdx.x >> 6);
   if (kvh >= a.Hkv) return;  // wave-uniform
   // the header and the bin's record load together (the record carries the segments' base): the
   // grid covers the plan's capacity, and workgroups past the step's nbins bins exit
@@ -265,11 +293,6 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
       qf[kk] = qvalid ? v : u32x4{0, 0, 0, 0};
     }
   };
-  // the segment's page ids, one per lane (pages 0-63 and 64-127 of the segment)
-  auto load_pages = [&](const int4& r0, int& lo, int& hi) {
-    lo = lane < r0.y ? a.kv_indices[r0.x + lane] : 0;
-    hi = lane + 64 < r0.y ? a.kv_indices[r0.x + 64 + lane] : 0;
-  };
 
   // The next segment's records, page ids and q are loaded whether or not there is a next segment (the
   // last one's again, unused), so no loaded value meets a branch join: a join would make the wave wait
@@ -278,13 +301,12 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
   int gi = bw.x;
   SegRec cur = seg_rec(segs, gi);
   SegRec nxt = seg_rec(segs, min(gi + 1, glast));
-  int page_lo, page_hi;
-  load_pages(cur.r0, page_lo, page_hi);
+  PageIds pages = load_page_ids(a.kv_indices, cur.r0, lane);
   u32x4 qf[4];
   load_q(cur.r1.x, qf);
   TileRegs<F8> tile, ahead;  // the tile being consumed, the one loaded ahead of it
   LoadCursor at;
-  load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+  load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, tile);
   at.advance(tpp);
 
   while (true) {
@@ -294,8 +316,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
     // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
     // only such pages has none
     const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
-    int next_lo, next_hi;
-    load_pages(nxt.r0, next_lo, next_hi);
+    const PageIds next_pages = load_page_ids(a.kv_indices, nxt.r0, lane);
     u32x4 next_q[4];
     load_q(nxt.r1.x, next_q);
     const SegRec after = seg_rec(segs, min(gi + 2, glast));
@@ -306,10 +327,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
     bool next_loaded = false;  // the next segment's first tile is on its way into `tile`
     for (int t = 0; t < ntiles; ++t) {
       if (t + 1 < ntiles) {
-        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, ahead);
+        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, ahead);
         at.advance(tpp);
       } else if (has_next) {
-        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, next_lo, next_hi, LoadCursor{}, c, g, ahead);
+        load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, next_pages, LoadCursor{}, c, g, ahead);
         next_loaded = true;
       }
       if constexpr (F8) {
@@ -354,13 +375,12 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(OCC
     ++gi;
     cur = nxt;
     nxt = after;
-    page_lo = next_lo;
-    page_hi = next_hi;
+    pages = next_pages;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = next_q[kk];
     at = LoadCursor{};
     if (!next_loaded)  // this segment had no tile to load it behind
-      load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+      load_tile<F8, NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, tile);
     at.advance(tpp);  // the new segment's first tile is in `tile`
   }
 }
@@ -387,9 +407,9 @@ struct PairTile {
 
 template <bool NT>
 __device__ __forceinline__ void load_pair(const DecodeArgs& a, const char* kbase, const char* vbase, int64_t tok_stride,
-                                          int64_t blk_stride, int page_lo, int page_hi, LoadCursor at, int c, int g,
+                                          int64_t blk_stride, const PageIds& pages, LoadCursor at, int c, int g,
                                           PairTile& r) {
-  int blk = __builtin_amdgcn_readlane(at.page < 64 ? page_lo : page_hi, at.page & 63);
+  int blk = page_id(pages, at.page);
   if ((unsigned)blk >= (unsigned)a.num_blocks) blk = 0;  // never taken with valid metadata; keeps reads in the pool
   const int64_t off = (int64_t)blk * blk_stride + (int64_t)(at.sub * 16) * tok_stride;
   const char* kp = kbase + off + c * tok_stride;
@@ -488,10 +508,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
       qb[t] = qvalid && in_b ? qv[t] : z;
     }
   };
-  auto load_pages = [&](const int4& r0, int& lo, int& hi) {
-    lo = lane < r0.y ? a.kv_indices[r0.x + lane] : 0;
-    hi = lane + 64 < r0.y ? a.kv_indices[r0.x + 64 + lane] : 0;
-  };
 
   const int64_t tok_stride = (int64_t)a.Hkv * kHeadDim;  // one byte per element
   const int64_t blk_stride = (int64_t)a.bs * tok_stride;
@@ -502,8 +518,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   int gi = bw.x;
   SegRec cur = seg_rec(segs, gi);
   SegRec nxt = seg_rec(segs, min(gi + 1, glast));
-  int page_lo, page_hi;
-  load_pages(cur.r0, page_lo, page_hi);
+  PageIds pages = load_page_ids(a.kv_indices, cur.r0, lane);
   u32x4 qa[4], qb[4];
   {
     u32x4 qv[4];
@@ -512,7 +527,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
   }
   PairTile tile, ahead;
   LoadCursor at;
-  load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+  load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, tile);
   at.advance(tpp);
 
   while (true) {
@@ -522,8 +537,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
     // pages past the row's last token (a block table may hold pages ahead) have no tiles: a segment of
     // only such pages has none
     const int ntiles = max(min(len, tok0 + cur.r0.y * a.bs) - tok0 + 15, 0) >> 4;
-    int next_lo, next_hi;
-    load_pages(nxt.r0, next_lo, next_hi);
+    const PageIds next_pages = load_page_ids(a.kv_indices, nxt.r0, lane);
     u32x4 next_q[4];
     load_q(nxt.r1.x, next_q);
     const SegRec after = seg_rec(segs, min(gi + 2, glast));
@@ -534,10 +548,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
     bool next_loaded = false;  // the next segment's first tile is on its way into `tile`
     for (int t = 0; t < ntiles; ++t) {
       if (t + 1 < ntiles) {
-        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, ahead);
+        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, ahead);
         at.advance(tpp);
       } else if (has_next) {
-        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, next_lo, next_hi, LoadCursor{}, c, g, ahead);
+        load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, next_pages, LoadCursor{}, c, g, ahead);
         next_loaded = true;
       }
       consume_pair<T>(tile, qa, qb, a.scale_log2, tok0 + t * 16, len, g, m_run, l_run, o);
@@ -582,12 +596,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
     ++gi;
     cur = nxt;
     nxt = after;
-    page_lo = next_lo;
-    page_hi = next_hi;
+    pages = next_pages;
     split_q(next_q, qa, qb);
     at = LoadCursor{};
     if (!next_loaded)  // this segment had no tile to load it behind
-      load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, page_lo, page_hi, at, c, g, tile);
+      load_pair<NT>(a, kbase, vbase, tok_stride, blk_stride, pages, at, c, g, tile);
     at.advance(tpp);
   }
 }
@@ -650,7 +663,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const int4* __rest
 }
 
 // Occupancy, tuned on MI355X (decode_256): every kernel loads one 16-token tile ahead of the one it
-// consumes.  The 16-bit kernel runs 3 wavefronts per SIMD (160 VGPRs, no spills).  With per-row splits, one tile
+// consumes.  The 16-bit kernel runs 3 wavefronts per SIMD (163 VGPRs, no spills) in workgroups of 4, or 2 per SIMD in
+// whole-page workgroups of 8.  With per-row splits, one tile
 // of lookahead at 3 per SIMD streamed as fast as two at 2 per SIMD, and the fp8 pair kernel ran the same
 // with one tile ahead as with two (192-195 us); the fp8 one-head kernel then ran 198 us with four tiles
 // ahead at 2 per SIMD against 205 us with one at 4.
@@ -684,11 +698,24 @@ __host__ __device__ constexpr bool pair_heads(int num_kv_heads, int group) {
 // Bins a plan of n_work records can hold: a header, then per bin one record and at least one segment
 // of two records.  The grid covers that many bins; the workgroups past the step's own exit at once.
 constexpr int max_bins(int n_work) { return n_work >= 4 ? (n_work - 1) / 3 : 0; }
+// Partial slots a plan of n_work records can use: a cut row takes one slot per segment, and the segments
+// take two records each after the header, so slots <= segments <= (n_work - 1) / 2.  The workspace holds
+// that many slots: acc[slot][head][Dh], then (m, l)[slot][head].
+constexpr int partial_slots(int n_work) { return n_work >= 1 ? (n_work - 1) / 2 : 0; }
 
 template <typename T, bool F8>
-int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
+int launch(const DecodeArgs& a, int n_work, int pages_per_split, hipStream_t st) {
   const unsigned bins = (unsigned)max_bins(n_work);
   if (bins == 0) return MLLM_OK;
+  if constexpr (!F8) {
+    if (whole_page(false, a.Hkv, pages_per_split)) {
+      DecodeArgs b = a;
+      b.HG = a.Hkv / kWavesWhole;
+      decode_kernel<T, false, kNonTemporal, kOccupancyWhole, kWavesWhole>
+          <<<bins * (unsigned)b.HG, 64 * kWavesWhole, 0, st>>>(b);
+      return check_launch("mllm_paged_decode");
+    }
+  }
   if constexpr (F8) {
     if (pair_heads(a.Hkv, a.G)) {
       DecodeArgs b = a;
@@ -697,7 +724,7 @@ int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
       return check_launch("mllm_paged_decode_fp8");
     }
   }
-  decode_kernel<T, F8, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy><<<bins * (unsigned)a.HG, 64 * kWaves, 0, st>>>(a);
+  decode_kernel<T, F8, kNonTemporal, F8 ? kOccupancyFp8 : kOccupancy, kWaves><<<bins * (unsigned)a.HG, 64 * kWaves, 0, st>>>(a);
   return check_launch(F8 ? "mllm_paged_decode_fp8" : "mllm_paged_decode");
 }
 
@@ -706,7 +733,7 @@ int launch(const DecodeArgs& a, int n_work, hipStream_t st) {
 
 extern "C" int64_t mllm_decode_workspace_bytes(int32_t num_decode_work, int32_t num_heads, int32_t head_dim) {
   if (num_decode_work <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  return (int64_t)num_decode_work * num_heads * ((int64_t)head_dim * 4 + 8);
+  return (int64_t)mllm::partial_slots(num_decode_work) * num_heads * ((int64_t)head_dim * 4 + 8);
 }
 
 namespace {
@@ -732,8 +759,8 @@ int paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
                fn + ": num_heads must be a multiple of num_kv_heads");
   MLLM_REQUIRE(num_heads / num_kv_heads <= 16, MLLM_ERR_UNSUPPORTED,
                fn + ": at most 16 query heads per KV head");
-  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
-               fn + ": pages_per_split must be in [1, 128]");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= kMaxSplitPages, MLLM_ERR_INVALID,
+               fn + ": pages_per_split must be in [1, 192]");
   MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0, MLLM_ERR_INVALID, fn + ": negative count");
   if (num_decode_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && decode_work,
@@ -771,11 +798,14 @@ int paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   a.o_sh = out_stride_head;
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
-                                        (int64_t)num_decode_work * num_heads * head_dim * 4);
+                                        (int64_t)partial_slots(num_decode_work) * num_heads * head_dim * 4);
   (void)merge_work;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == MLLM_DTYPE_BF16) return fp8 ? launch<BF16, true>(a, num_decode_work, st) : launch<BF16, false>(a, num_decode_work, st);
-  return fp8 ? launch<F16, true>(a, num_decode_work, st) : launch<F16, false>(a, num_decode_work, st);
+  if (dtype == MLLM_DTYPE_BF16)
+    return fp8 ? launch<BF16, true>(a, num_decode_work, pages_per_split, st)
+               : launch<BF16, false>(a, num_decode_work, pages_per_split, st);
+  return fp8 ? launch<F16, true>(a, num_decode_work, pages_per_split, st)
+             : launch<F16, false>(a, num_decode_work, pages_per_split, st);
 }
 
 }  // namespace
@@ -816,7 +846,7 @@ int launch_merge(const int32_t* merge_work, int32_t num_merge_work, int32_t num_
   using namespace mllm;
   const float* part_o = static_cast<const float*>(workspace);
   const float2* part_ml = reinterpret_cast<const float2*>(static_cast<const char*>(workspace) +
-                                                          (int64_t)num_decode_work * num_heads * kHeadDim * 4);
+                                                          (int64_t)partial_slots(num_decode_work) * num_heads * kHeadDim * 4);
   dim3 grid(num_merge_work, (num_heads + kMergeHeads - 1) / kMergeHeads);
   const int4* merge = reinterpret_cast<const int4*>(merge_work);
   if (dtype == MLLM_DTYPE_BF16)
@@ -888,10 +918,10 @@ int scratch_ptr(void** out) {
   return MLLM_OK;
 }
 
-// Plan records (partial slots) whose partials fit in the scratch.
+// The most plan records whose partial slots fit in the scratch (two records per slot, plus the header).
 int64_t noalloc_max_work(int32_t num_heads, int32_t head_dim) {
-  const int64_t per = mllm_decode_workspace_bytes(1, num_heads, head_dim);
-  return per > 0 ? kScratchBytes / per : 0;
+  const int64_t per_slot = mllm_decode_workspace_bytes(3, num_heads, head_dim);  // 3 records: one slot
+  return per_slot > 0 ? 2 * (kScratchBytes / per_slot) + 2 : 0;
 }
 
 }  // namespace

@@ -15,7 +15,7 @@ namespace mllm {
 namespace {
 
 constexpr int kPlanThreads = 1024;
-constexpr int kMaxSplitPages = 128;
+constexpr int kMaxSplitPages = 192;  // pages a decode segment's page-id registers hold
 constexpr int kPrefillKeyTile = 64;               // keys per tile of the prefill kernel (its cost unit)
 constexpr int kPrefillClasses = kPlanThreads;     // prefill size classes: 1 .. 1023 tiles, the last one open
 
@@ -63,7 +63,7 @@ __device__ __forceinline__ int bin_of(int64_t p, int64_t total, int nb) {
   return b;
 }
 
-// split_dev: when not null, the split size is read from device memory (clamped to [pages_per_split, 128]:
+// split_dev: when not null, the split size is read from device memory (clamped to [pages_per_split, 192]:
 // the capacities were sized for pages_per_split, so no item is ever dropped).
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ qo_indptr,
                                                             const int32_t* __restrict__ kv_indptr,
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
       // a step larger than the capacities gets no decode work at all, so the decode and merge kernels
       // never index past a workspace sized for cap_decode partial slots
       fits = nb > 0 && 1 + (int64_t)nb + 2 * (int64_t)n_seg <= cap_decode && n_merge <= cap_merge &&
-             n_slot <= cap_decode;
+             n_slot <= (cap_decode - 1) / 2;  // the workspace holds (records - 1) / 2 partial slots
     }
   }
   // header: {nb, segments, partial slots, 0}; a step with decode pages that does not fit reports what it
@@ -206,8 +206,8 @@ int plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* seq_
   using namespace mllm;
   const std::string f = fn;
   MLLM_REQUIRE(num_seqs >= 0, MLLM_ERR_INVALID, f + ": num_seqs < 0");
-  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= 128, MLLM_ERR_INVALID,
-               f + ": pages_per_split must be in [1, 128]");
+  MLLM_REQUIRE(pages_per_split >= 1 && pages_per_split <= kMaxSplitPages, MLLM_ERR_INVALID,
+               f + ": pages_per_split must be in [1, 192]");
   MLLM_REQUIRE(q_tile_tokens >= 1, MLLM_ERR_INVALID, f + ": q_tile_tokens must be positive");
   MLLM_REQUIRE(num_decode_work >= 0 && num_merge_work >= 0 && num_prefill_work >= 0, MLLM_ERR_INVALID,
                f + ": negative capacity");

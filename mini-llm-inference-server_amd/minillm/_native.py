@@ -16,12 +16,23 @@ LIB_PATH = Path(os.environ.get("MLLM_HIP_LIB", Path(__file__).resolve().parent /
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
+
+
+class LayerStep(ctypes.Structure):
+    """mllm_layer_step: the step-constant arguments of mllm_attention_forward (same fields, same order)."""
+
+    _fields_ = [("num_blocks", _i64), ("num_tokens", _i64), ("slot_mapping", _p), ("qo_indptr", _p),
+                ("kv_indptr", _p), ("kv_indices", _p), ("seq_lens", _p), ("decode_work", _p), ("merge_work", _p),
+                ("prefill_work", _p), ("workspace", _p), ("workspace_bytes", _i64), ("num_decode_work", _i32),
+                ("num_merge_work", _i32), ("num_prefill_work", _i32), ("pages_per_split", _i32),
+                ("q_tile_tokens", _i32), ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
+                ("block_size", _i32), ("dtype", _i32), ("kv_fp8", _i32), ("softmax_scale", _f32)]
 
 # symbol -> (restype, argtypes); the exact list include/minillm_hip.h declares
 SIGNATURES = {
@@ -45,6 +56,9 @@ SIGNATURES = {
     # decode + merge with the partials in the library's own scratch array (no allocation)
     "mllm_paged_decode_noalloc": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
                                                  _p, _i32, _p, _i32, _i32, _f32, _i32, _p, _i64, _i64, _p]),
+    # one layer: append (RoPE optionally fused), decode + merge, prefill
+    "mllm_attention_forward": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p,
+                                              _p, _p, _f32, _f32, _p, _p]),
     "mllm_paged_prefill": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                           _i32, _i32, _f32, _i32, _p, _i64, _i64, _p]),
     "mllm_dense_attention": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
@@ -83,6 +97,13 @@ class NativeLib:
 
     def last_error(self) -> str:
         return (self._cdll.mllm_last_error() or b"").decode()
+
+    def fn(self, name: str):
+        """The typed foreign function itself, for callers that check its status with `check`."""
+        return getattr(self._cdll, name)
+
+    def check(self, status: int) -> None:
+        self._check(status)
 
     def _check(self, status: int) -> None:
         if status == OK:

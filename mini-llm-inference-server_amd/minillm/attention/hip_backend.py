@@ -20,6 +20,7 @@ to `forward`; q, k, v and the output stay bf16 / fp16.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from dataclasses import dataclass
@@ -31,6 +32,7 @@ from .base import AttentionBackend
 from .metadata import decode_plan_size
 
 FULL_CHIP_CUS = 256  # MI355X: 8 XCDs x 32 CUs
+MAX_SPLIT_PAGES = 192  # pages one decode bin may hold (the kernels keep a segment's page ids in 3 registers)
 _CUS: dict = {}
 
 
@@ -48,10 +50,19 @@ def device_cus(device=None) -> int:
     return cus
 
 
+WHOLE_PAGE_WAVES = 8  # KV heads per workgroup of the whole-page decode launch (one workgroup per CU)
+WHOLE_PAGE_MIN_SPLIT = 24  # the library launches it from this split size up (kWholePageMinSplit)
+
+
+def whole_page(kv_fp8: bool, num_kv_heads: int, split: int) -> bool:
+    """Whether mllm_paged_decode runs its whole-page workgroups for this split size (the library's rule)."""
+    return not kv_fp8 and num_kv_heads % WHOLE_PAGE_WAVES == 0 and split >= WHOLE_PAGE_MIN_SPLIT
+
+
 def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int = FULL_CHIP_CUS) -> tuple[int, int]:
-    """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes): CUs x 4 SIMDs x 3
-    per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two KV heads
-    when they pair up (decode_kernel_name), else one per KV head."""
+    """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes) for the kernels of
+    small steps: CUs x 4 SIMDs x 3 per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8
+    kernels, one per two KV heads when they pair up (decode_kernel_name), else one per KV head."""
     if not kv_fp8:
         return num_cus * 4 * 3, num_kv_heads
     if decode_kernel_name(True, num_heads, num_kv_heads) == "decode_pair_kernel":
@@ -60,19 +71,32 @@ def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int =
 
 
 def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None = None, kv_fp8: bool = False,
-                    num_cus: int = FULL_CHIP_CUS) -> int:
-    """Pages per decode bin: the step's bins make one round of the kernel's resident wavefronts on a device
-    of `num_cus` CUs, clamped to [8, 128] pages (~89 pages on the 256-row decode workload with a bf16 pool
-    on the full chip, ~67 with an fp8 one).  More rounds of smaller bins measured slower (60 and 45 pages
-    on bf16 decode_256: +10% and +7%), and so do bins that leave resident wavefronts idle (fp8 pool at 89
-    pages: +10%).  Below the clamp, small steps gain nothing: decode + merge over 8 / 32 / 64 rows of
-    U[128, 4096] tokens took 27 / 56 / 99 us with this choice against 30 / 74 / 140 us at 4 pages and
-    63 / 125 / 219 us at 1 page; 4 rows take ~16.5 us at every size from 1 to 8 pages (launch latency)."""
+                    num_cus: int = FULL_CHIP_CUS, whole_pages: bool = True) -> int:
+    """Pages per decode bin, so that the step's bins make one round of the decode launch's resident
+    workgroups on a device of `num_cus` CUs.
+
+    16-bit pools with KV heads in groups of 8 (`whole_pages`): one whole-page workgroup per CU, Hkv / 8 per
+    bin, so bins of ceil(T / (rounds x bins per round)) pages, at most 192 (two rounds past 192 x 256 pages).
+    That is 134 pages on the 256-row decode workload: 255 bins, 341.7 us against 349.6 us for 383 bins of 89
+    pages in 4-wavefront workgroups (with 257 bins of 133 pages, one bin past a round, 554 us).  When that
+    size is below WHOLE_PAGE_MIN_SPLIT the library runs 4-wavefront workgroups at 3 per SIMD instead, and
+    the bins make one round of those (CUs x 12 wavefronts, one per KV head), at least 8 pages: more rounds of
+    smaller bins measured slower (60 and 45 pages on bf16 decode_256: +10% and +7%), and below 8 pages small
+    steps gain nothing (decode + merge over 8 / 32 / 64 rows of U[128, 4096] tokens took 27 / 56 / 99 us at
+    this size against 30 / 74 / 140 us at 4 pages; 4 rows take ~16.5 us at 1 to 8 pages, launch latency).
+    fp8 pools size their bins for their own kernels' occupancy (67 pages on decode_256 for the pair kernel).
+    `whole_pages=False` gives the 4-wavefront sizing whatever the step."""
     forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
     if forced:
-        return max(1, min(128, int(forced)))
+        return max(1, min(MAX_SPLIT_PAGES, int(forced)))
+    if whole_pages and not kv_fp8 and num_kv_heads % WHOLE_PAGE_WAVES == 0 and decode_pages > 0:
+        per_round = max(1, num_cus // (num_kv_heads // WHOLE_PAGE_WAVES))
+        rounds = math.ceil(decode_pages / (MAX_SPLIT_PAGES * per_round))
+        split = math.ceil(decode_pages / (rounds * per_round))
+        if split >= WHOLE_PAGE_MIN_SPLIT:
+            return split
     slots, per_bin = decode_waves(num_heads or 4 * num_kv_heads, num_kv_heads, kv_fp8, num_cus)
-    return max(8, min(128, math.ceil(decode_pages * per_bin / slots)))
+    return max(8, min(MAX_SPLIT_PAGES, math.ceil(decode_pages * per_bin / slots)))
 
 
 class PlanOverflowError(RuntimeError):
@@ -107,6 +131,11 @@ class StepPlan:
     # qo_indptr, kv_indptr, kv_indices, seq_lens_i32, then the work lists and their sizes
     meta_ptrs: tuple = ()
     decode_args: tuple = ()
+    # the mllm_layer_step of mllm_attention_forward, built on the plan's first layer call and rebuilt when
+    # the pools' shape, the dtypes or the workspace change
+    layer_key: tuple | None = None
+    layer_step: object = None
+    layer_addr: int = 0
 
 
 def _ptr(t: torch.Tensor | None) -> int:
@@ -151,6 +180,7 @@ class HipBackend(AttentionBackend):
 
     def __init__(self) -> None:
         self._lib = _native.lib()
+        self._attention_forward = self._lib.fn("mllm_attention_forward")
         self._planned = None  # the AttentionMetadata the plan was last built for
         self._planned_fp8 = False  # and the pool type it was built for
         self._plan: StepPlan | None = None
@@ -161,10 +191,58 @@ class HipBackend(AttentionBackend):
 
     def forward(self, q, k, v, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):
         q, k, v = self._check(q, k, v, k_cache, v_cache, meta, k_scale, v_scale)
-        self.append(k, v, k_cache, v_cache, meta, k_scale, v_scale)
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        self.attend(q, k_cache, v_cache, meta, out, k_scale, v_scale)
+        if self._split_launches(q, k_cache, meta):
+            self.append(k, v, k_cache, v_cache, meta, k_scale, v_scale)
+            self.attend(q, k_cache, v_cache, meta, out, k_scale, v_scale)
+        else:
+            self.run_layer(q, k, v, k_cache, v_cache, meta, out, k_scale=k_scale, v_scale=v_scale)
         return out
+
+    def _split_launches(self, q, k_cache, meta) -> bool:
+        """Whether this layer runs as separate calls: only a mixed step with `overlap_mixed` set, whose
+        prefill goes to a second stream."""
+        if not self.overlap_mixed:
+            return False
+        plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device, is_fp8(k_cache))
+        return bool(plan.num_decode and plan.num_prefill) and not torch.cuda.is_current_stream_capturing()
+
+    def run_layer(self, q, k, v, k_cache, v_cache, meta, out, cos=None, sin=None, q_rot=None,
+                  k_scale: float = 1.0, v_scale: float = 1.0) -> None:
+        """The layer's whole path in one host call (mllm_attention_forward): KV append (with cos and sin, the
+        RoPE of q and k fused into it and the rotated q written to q_rot), decode + merge, prefill, on the
+        current stream.  The arguments are the checked ones of `forward` / `forward_rotary`; q_rot and out
+        are contiguous [N, H, Dh]."""
+        fp8 = is_fp8(k_cache)
+        plan = self.plan(meta, q.shape[1], k_cache.shape[2], q.shape[2], q.device, fp8)
+        step = self._layer_step(plan, meta, q, k_cache, fp8)
+        rot = cos is not None
+        self._lib.check(self._attention_forward(
+            step, q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(),
+            v.stride(0), v.stride(1), cos.data_ptr() if rot else None, sin.data_ptr() if rot else None,
+            cos.stride(0) if rot else 0, q_rot.data_ptr() if rot else None, k_cache.data_ptr(), v_cache.data_ptr(),
+            k_scale, v_scale, out.data_ptr(), _native.stream_ptr(q.device)))
+
+    def _layer_step(self, plan: StepPlan, meta, q, k_cache, fp8: bool) -> int:
+        """Address of the plan's mllm_layer_step for these pools and this workspace."""
+        ws = self._workspace
+        key = (k_cache.shape[0], k_cache.shape[1], q.dtype, fp8, ws.data_ptr() if ws is not None else 0)
+        if plan.layer_key == key:
+            return plan.layer_addr
+        ws = self._workspace_for(plan.workspace_bytes, q.device)
+        num_blocks, bs, hkv, dh = k_cache.shape
+        step = _native.LayerStep(
+            num_blocks=num_blocks, num_tokens=q.shape[0], slot_mapping=meta.slot_mapping.data_ptr(),
+            qo_indptr=plan.meta_ptrs[0], kv_indptr=plan.meta_ptrs[1], kv_indices=plan.meta_ptrs[2],
+            seq_lens=plan.meta_ptrs[3], decode_work=_ptr(plan.decode_work), merge_work=_ptr(plan.merge_work),
+            prefill_work=_ptr(plan.prefill_work), workspace=_ptr(ws), workspace_bytes=plan.workspace_bytes,
+            num_decode_work=plan.num_decode, num_merge_work=plan.num_merge, num_prefill_work=plan.num_prefill,
+            pages_per_split=plan.pages_per_split, q_tile_tokens=plan.q_tile, num_heads=q.shape[1],
+            num_kv_heads=hkv, head_dim=dh, block_size=bs, dtype=_native.dtype_code(q.dtype), kv_fp8=int(fp8),
+            softmax_scale=dh ** -0.5)
+        plan.layer_step, plan.layer_addr = step, ctypes.addressof(step)
+        plan.layer_key = (num_blocks, bs, q.dtype, fp8, ws.data_ptr() if ws is not None else 0)
+        return plan.layer_addr
 
     def _check(self, q, k, v, k_cache, v_cache, meta, k_scale=1.0, v_scale=1.0):
         n, h, dh = q.shape
@@ -201,9 +279,21 @@ class HipBackend(AttentionBackend):
         cos / sin rows [N, Dh].  One launch rotates q and k, appends the rotated k and v to the pool and
         writes the rotated q, bit for bit what apply_rotary followed by `forward` produces."""
         q, k, v = self._check(q, k, v, k_cache, v_cache, meta, k_scale, v_scale)
-        q_rot = self.rope_append(q, k, v, cos, sin, k_cache, v_cache, meta, k_scale, v_scale)
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        self.attend(q_rot, k_cache, v_cache, meta, out, k_scale, v_scale)
+        if self._split_launches(q, k_cache, meta):
+            q_rot = self.rope_append(q, k, v, cos, sin, k_cache, v_cache, meta, k_scale, v_scale)
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+            self.attend(q_rot, k_cache, v_cache, meta, out, k_scale, v_scale)
+            return out
+        n, h, dh = q.shape
+        if cos.shape != (n, dh) or sin.shape != (n, dh):
+            raise ValueError(f"cos and sin must be [N, Dh] = [{n}, {dh}]")
+        if cos.dtype != q.dtype or sin.dtype != q.dtype:
+            raise ValueError("q, cos, sin and the pools must share one dtype (or the pools be fp8)")
+        if cos.stride(-1) != 1 or sin.stride() != cos.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        q_rot = torch.empty((n, h, dh), dtype=q.dtype, device=q.device)
+        out = torch.empty((n, h, dh), dtype=q.dtype, device=q.device)
+        self.run_layer(q, k, v, k_cache, v_cache, meta, out, cos, sin, q_rot, k_scale, v_scale)
         return out
 
     def rope_append(self, q, k, v, cos, sin, k_cache, v_cache, meta, k_scale: float = 1.0, v_scale: float = 1.0):

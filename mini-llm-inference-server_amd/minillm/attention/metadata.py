@@ -297,7 +297,7 @@ class StaticDecodeMetadata:
 
     def split_size(self, pages_per_split: int) -> int:
         """The split size a staged step runs with (what mllm_plan_dev clamps it to)."""
-        return max(self.SPLIT_MIN, min(128, int(pages_per_split)))
+        return max(self.SPLIT_MIN, min(192, int(pages_per_split)))
 
     def load(self, keys, seqs: list[SeqStep], pages_per_split: int = SPLIT_MIN) -> None:
         """Stages a decode step (len(seqs) <= num_rows) and its split size for the next build: host packing,

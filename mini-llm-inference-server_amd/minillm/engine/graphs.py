@@ -28,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from ..attention.hip_backend import device_cus, pages_per_split
+from ..attention.hip_backend import MAX_SPLIT_PAGES, device_cus, pages_per_split
 from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata, decode_plan_size
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
@@ -84,7 +84,7 @@ class DecodeGraphs:
             return False
         b = self.bucket(len(seqs))
         pages = sum(-(-(s.num_cached + 1) // self.block_size) for s in seqs)
-        c = max(StaticDecodeMetadata.SPLIT_MIN, min(128, self._split(pages)))
+        c = max(StaticDecodeMetadata.SPLIT_MIN, min(MAX_SPLIT_PAGES, self._split(pages)))
         records, _ = decode_plan_size(pages + (b - len(seqs)), b, c)  # padding rows hold one page each
         if records <= self.capacity(b):
             return True
@@ -112,7 +112,10 @@ class DecodeGraphs:
     # ------------------------------------------------------------------ internals
 
     def _split(self, pages: int) -> int:
-        """The split size an eager step over `pages` decode pages uses with this pool."""
+        """The split size an eager step over `pages` decode pages uses with this pool.  A replay cuts the same
+        bins, so its output is the eager step's bit for bit; its decode launch, planned at the smallest
+        split, runs 4-wavefront workgroups over them (the launch shape does not change a wavefront's
+        arithmetic)."""
         return pages_per_split(pages, self.num_kv_heads, self.num_heads, self.cache.quantized,
                                device_cus(self.device))
 

@@ -155,6 +155,54 @@ def test_mixed_step_overlap_is_bit_identical(hip):
     assert torch.equal(bits(outs[0]), bits(outs[1]))
 
 
+@pytest.mark.parametrize("pool", ["bf16", "fp8"])
+@pytest.mark.parametrize("rotary", [False, True])
+def test_one_call_layer_equals_separate_launches(hip, pool, rotary):
+    # mllm_attention_forward (forward / forward_rotary's single host call) against the same launches made
+    # one entry point at a time (append or RoPE + append, decode, merge, prefill): pools, rotated q and
+    # output bit for bit, on a step with every row kind
+    from minillm import workloads
+    from minillm.attention.hip_backend import HipBackend
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+    from minillm.model.config import LLAMA_3_1_8B, LlamaConfig
+    from minillm.model.llama import RotaryEmbedding
+
+    wl = workloads.mixed_128()
+    fp8 = pool == "fp8"
+    ks, vs = (0.75, 1.25) if fp8 else (1.0, 1.0)
+    results = []
+    for one_call in (True, False):
+        be = HipBackend()
+        meta = AttentionMetadata.build([SeqStep(c, n, list(b)) for c, n, b in wl.seqs], wl.block_size, DEV)
+        q, k, v = wl.q.to(DEV), wl.k.to(DEV), wl.v.to(DEV)
+        pk, pv = wl.pool_k.to(DEV), wl.pool_v.to(DEV)
+        if fp8:
+            pk, pv = pk.to(torch.float8_e4m3fn), pv.to(torch.float8_e4m3fn)
+        cos = sin = None
+        if rotary:
+            cos, sin = RotaryEmbedding(LlamaConfig(**LLAMA_3_1_8B))(meta.positions[None], q.dtype)
+            cos, sin = cos[0], sin[0]
+        out = torch.full_like(q, float("nan"))
+        q_rot = torch.full_like(q, float("nan")) if rotary else None
+        if one_call:
+            be.run_layer(q, k, v, pk, pv, meta, out, cos, sin, q_rot, ks, vs)
+        else:
+            qa = q
+            if rotary:
+                qa = q_rot = be.rope_append(q, k, v, cos, sin, pk, pv, meta, ks, vs)
+            else:
+                be.append(k, v, pk, pv, meta, ks, vs)
+            be.attend(qa, pk, pv, meta, out, ks, vs)
+        torch.cuda.synchronize()
+        results.append((out, q_rot, pk, pv))
+    (o1, r1, k1, v1), (o2, r2, k2, v2) = results
+    assert torch.isfinite(o1).all()
+    assert torch.equal(bits(o1), bits(o2))
+    assert torch.equal(k1.view(torch.uint8), k2.view(torch.uint8)) and torch.equal(v1.view(torch.uint8), v2.view(torch.uint8))
+    if rotary:
+        assert torch.equal(bits(r1), bits(r2))
+
+
 def test_fp16_pool_parity(hip):
     from minillm import workloads
 
@@ -501,6 +549,73 @@ def test_decode_rows_with_pages_past_their_last_token(hip, pages_per_split):
     assert dec[0].item() == -(-total // pages_per_split)  # the plan fit its capacity
     assert torch.isfinite(out).all()
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("pages_per_split", [128, 150, 192])
+def test_decode_bins_of_up_to_192_pages(hip, monkeypatch, pages_per_split):
+    # a bin holds up to 192 pages (three page-id registers per lane): long decode rows cut into such bins,
+    # bf16 and fp8 pools (the one-head and the pair kernels), against the oracle
+    from minillm.attention.hip_backend import HipBackend
+
+    rng = random.Random(pages_per_split)
+    steps = [(rng.randrange(1500, 7000), 1) for _ in range(24)] + [(rng.randrange(0, 200), 1) for _ in range(8)]
+    nb = sum(-(-(c + n) // 16) for c, n in steps) + 8
+    wl = _kernel_case(h=32, hkv=8, steps=steps, num_blocks=nb, seed=pages_per_split)
+    monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", str(pages_per_split))
+    be = HipBackend()
+    out, pk, pv, meta = hip_step(wl, DEV, backend=be)
+    assert be._plan.pages_per_split == pages_per_split
+    segs = be._plan.decode_work.view(-1, 4)[1 + be._plan.decode_work[0].item():].cpu()
+    longest = segs[0::2][:, 1].max().item()  # bins hold floor or ceil(T / bins) pages: some segment fills one
+    assert pages_per_split - 1 <= longest <= pages_per_split and longest > 127
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+    from test_gpu_fp8 import _check, fp8_step
+
+    _check(*fp8_step(wl, 0.5, 2.0))  # the pair kernel (two KV heads per wavefront)
+
+
+@pytest.mark.parametrize("h,hkv", [(32, 8), (64, 16)])
+def test_whole_page_launch_equals_four_wave_launch(hip, h, hkv):
+    # the library picks whole-page workgroups (8 KV heads each, one per CU) from 24 pages a bin up and
+    # 4-wavefront workgroups below; over the same plan the two launch shapes give the same bits (each
+    # wavefront's arithmetic is the same), and both match the oracle
+    from minillm import _native
+    from minillm.attention.hip_backend import HipBackend, _ptr, whole_page
+    from minillm.attention.metadata import AttentionMetadata, SeqStep
+
+    rng = random.Random(hkv)
+    steps = [(rng.randrange(100, 3000), 1) for _ in range(96)] + [(rng.randrange(0, 40), rng.randrange(2, 90))
+                                                                  for _ in range(3)]
+    nb = sum(-(-(c + n) // 16) for c, n in steps) + 8
+    wl = _kernel_case(h=h, hkv=hkv, steps=steps, num_blocks=nb, seed=hkv)
+    be = HipBackend()
+    meta = AttentionMetadata.build([SeqStep(c, n, list(b)) for c, n, b in wl.seqs], wl.block_size, DEV)
+    q, k, v = wl.q.to(DEV), wl.k.to(DEV), wl.v.to(DEV)
+    pk, pv = wl.pool_k.to(DEV), wl.pool_v.to(DEV)
+    be.append(k, v, pk, pv, meta)
+    plan = be.plan(meta, h, hkv, 128, torch.device(DEV))
+    assert whole_page(False, hkv, plan.pages_per_split)  # the backend sized this step for whole pages
+    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=DEV)
+    lib, st = _native.lib(), _native.stream_ptr(DEV)
+    outs = []
+    for split_arg in (plan.pages_per_split, 8):  # the same plan, launched whole-page, then 4-wavefront
+        assert whole_page(False, hkv, split_arg) == (split_arg >= 24)
+        out = torch.full_like(q, float("nan"))
+        lib.call("mllm_paged_decode", q.data_ptr(), q.stride(0), q.stride(1), pk.data_ptr(), pv.data_ptr(),
+                 pk.shape[0], 16, h, hkv, 128, *plan.meta_ptrs, _ptr(plan.decode_work), plan.num_decode,
+                 _ptr(plan.merge_work), plan.num_merge, split_arg, 128 ** -0.5, _native.dtype_code(q.dtype),
+                 out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), st)
+        lib.call("mllm_merge_splits", _ptr(plan.merge_work), plan.num_merge, plan.num_decode, h, 128,
+                 meta.qo_indptr.data_ptr(), _native.dtype_code(q.dtype), out.data_ptr(), out.stride(0),
+                 out.stride(1), ws.data_ptr(), ws.numel(), st)
+        outs.append(out)
+    torch.cuda.synchronize()
+    rows = torch.tensor([i for i, (c, n) in enumerate(steps) if n == 1], device=DEV)  # decode rows: q row = i
+    assert torch.equal(bits(outs[0][rows]), bits(outs[1][rows]))
+    ref, _, _ = oracle_step(wl, DEV)
+    torch.testing.assert_close(outs[0][rows].float(), ref[rows].float(), atol=ATOL, rtol=RTOL)
 
 
 def test_plan_overflow_is_reported(hip):

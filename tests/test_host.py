@@ -52,7 +52,8 @@ def test_bindings_cover_the_header(libpath):
     assert set(_native.SIGNATURES) == declared_symbols()
     lib = _native.lib()  # loads without a GPU; checks the ABI version
     assert lib.last_error() == ""
-    assert lib.workspace_bytes(10, 32, 128) == 10 * 32 * (128 * 4 + 8)
+    assert lib.workspace_bytes(10, 32, 128) == 4 * 32 * (128 * 4 + 8)  # (10 - 1) // 2 partial slots
+    assert lib.workspace_bytes(3, 32, 128) == 32 * (128 * 4 + 8) and lib.workspace_bytes(2, 32, 128) == 0
     assert lib.workspace_bytes(0, 32, 128) == 0
 
 
@@ -75,6 +76,51 @@ def test_argument_errors_map_to_value_error(libpath):
     lib.call("mllm_paged_decode", 0, 0, 0, 0, 0, 0, 16, 32, 8, 128, 0, 0, 0, 0, 0, 0, 0, 0, 8, 1.0, 2, 0, 0, 0, 0, 0, 0)
 
 
+def test_layer_step_struct_matches_the_header(tmp_path):
+    # the ctypes mirror of mllm_layer_step has the C struct's size and every field at the C offset
+    import ctypes
+
+    from minillm import _native
+
+    fields = [name for name, _ in _native.LayerStep._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"minillm_hip.h\"\nint main(void) {\n"
+                   + 'printf("%zu\\n", sizeof(mllm_layer_step));\n'
+                   + "".join(f'printf("%zu\\n", offsetof(mllm_layer_step, {f}));\n' for f in fields)
+                   + "return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_native.LayerStep)
+    assert got[1:] == [getattr(_native.LayerStep, f).offset for f in fields]
+
+
+def test_attention_forward_argument_errors(libpath):
+    # mllm_attention_forward checks its own arguments and those of the launches it makes, before any launch
+    from minillm import _native
+
+    lib = _native.lib()
+    fwd = lib.fn("mllm_attention_forward")
+    args = [0, 0, 0, 0, 0, 0, 0, 0, 0, None, None, 0, None, 0, 0, 1.0, 1.0, 0, None]  # q .. stream
+    with pytest.raises(ValueError, match="null step"):
+        lib.check(fwd(None, *args))
+    step = _native.LayerStep(num_heads=32, num_kv_heads=8, head_dim=128, block_size=16, dtype=2, softmax_scale=0.1)
+    with pytest.raises(ValueError, match="fp8 pools only"):
+        lib.check(fwd(ctypes_addr(step), *args[:15], 0.5, 1.0, *args[17:]))
+    with pytest.raises(ValueError, match="go together"):
+        lib.check(fwd(ctypes_addr(step), *args[:9], 1 << 20, None, *args[11:]))
+    lib.check(fwd(ctypes_addr(step), *args))  # no tokens and no work: a no-op that launches nothing
+    step.dtype = 0
+    with pytest.raises(ValueError, match="dtype"):
+        lib.check(fwd(ctypes_addr(step), *args[:9], 1 << 20, 1 << 20, 0, 1 << 20, *args[13:]))
+
+
+def ctypes_addr(obj) -> int:
+    import ctypes
+
+    return ctypes.addressof(obj)
+
+
 def test_registry():
     from minillm.attention import get_backend
 
@@ -92,13 +138,30 @@ def test_metadata_short_table_raises_before_touching_a_device():
 
 
 def test_split_size_heuristic(monkeypatch):
+    import math
+
     from minillm.attention import hip_backend
 
     monkeypatch.delenv("MLLM_PAGES_PER_SPLIT", raising=False)
     assert hip_backend.pages_per_split(10, 8) == 8
-    assert hip_backend.pages_per_split(10 ** 7, 8) == 128
+    assert hip_backend.pages_per_split(10 ** 7, 8) == 192
+    # whole-page workgroups, one per CU: at most 256 bins, one round
     c = hip_backend.pages_per_split(34000, 8)
-    assert 80 <= c <= 100  # one round of the 16-bit kernel's 3,072 wavefronts, one per KV head per bin
+    assert c == 133 and math.ceil(34000 / c) <= 256 and math.ceil(34000 / (c - 1)) > 256
+    assert hip_backend.whole_page(False, 8, c)
+    # two rounds past 192 x 256 pages
+    c = hip_backend.pages_per_split(65536, 8)
+    assert c == 128 and math.ceil(65536 / c) == 512
+    # below the whole-page threshold: one round of the 4-wavefront kernel's 3,072 wavefronts
+    c = hip_backend.pages_per_split(5000, 8)
+    assert c == math.ceil(5000 * 8 / 3072) == 14 and not hip_backend.whole_page(False, 8, c)
+    assert hip_backend.pages_per_split(34000, 8, whole_pages=False) == 89
+    # 16 KV heads: two whole-page workgroups per bin, 128 bins a round (here two rounds: 266 pages > 192)
+    assert hip_backend.pages_per_split(20000, 16, 64) == math.ceil(20000 / 128)
+    assert hip_backend.pages_per_split(34000, 16, 64) == math.ceil(34000 / 256)
+    # KV heads not in groups of 8 never take the whole-page launch
+    assert hip_backend.pages_per_split(34000, 4, 32) == math.ceil(34000 * 4 / 3072)
+    assert not hip_backend.whole_page(False, 4, 100) and not hip_backend.whole_page(True, 8, 100)
     assert hip_backend.pages_per_split(34000, 8, 32, kv_fp8=True) == 67  # fp8 pair kernel: 2,048, one per 2 heads
     assert hip_backend.pages_per_split(34000, 7, 28, kv_fp8=True) == 117  # fp8 one-head kernel: 2,048, one per head
     monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", "5")
@@ -122,10 +185,12 @@ def test_split_size_follows_the_device_cu_count(monkeypatch):
     assert hip_backend.device_cus(None) == hip_backend.FULL_CHIP_CUS
     full = hip_backend.pages_per_split(10000, 8, 32, False, hip_backend.device_cus("cuda:0"))
     part = hip_backend.pages_per_split(10000, 8, 32, False, hip_backend.device_cus("cuda:1"))
-    assert full == hip_backend.pages_per_split(10000, 8) == math.ceil(10000 * 8 / (256 * 12)) == 27
-    assert part == math.ceil(10000 * 8 / (64 * 12)) == 105
+    assert full == hip_backend.pages_per_split(10000, 8) == math.ceil(10000 / 256) == 40  # whole pages, one a CU
+    assert part == math.ceil(10000 / 64) == 157
+    assert hip_backend.pages_per_split(10000, 8, 32, False, 256, whole_pages=False) == math.ceil(10000 * 8 / 3072)
+    assert hip_backend.pages_per_split(10000, 8, 32, False, 64, whole_pages=False) == math.ceil(10000 * 8 / 768)
     assert hip_backend.pages_per_split(10000, 8, 32, True, 64) == math.ceil(10000 * 4 / (64 * 8)) == 79
-    assert hip_backend.pages_per_split(40000, 8, 32, False, 64) == 128  # clamped
+    assert hip_backend.pages_per_split(40000, 8, 32, False, 64, whole_pages=False) == 192  # clamped
 
 
 def test_workloads_are_deterministic_and_sized():
@@ -142,7 +207,7 @@ def test_workloads_are_deterministic_and_sized():
 
 def test_uniform_decode_workload_has_equal_full_rows():
     # decode_uniform_<rows>x<pages>: every row exactly `pages` full pages after the append, one new token,
-    # distinct pages; at 384 x 89 the split heuristic picks 89, so every row is one equal item
+    # distinct pages; at 384 x 89 the 4-wavefront sizing picks 89, so every row is one equal item
     from minillm import workloads
     from minillm.attention import hip_backend
 
@@ -151,7 +216,7 @@ def test_uniform_decode_workload_has_equal_full_rows():
     assert all(n == 1 and c + n == 5 * 16 and len(t) == 5 for c, n, t in w.seqs)
     used = [b for _, _, t in w.seqs for b in t]
     assert len(set(used)) == len(used) and max(used) < w.num_blocks == 60
-    assert hip_backend.pages_per_split(384 * 89, 8) == 89
+    assert hip_backend.pages_per_split(384 * 89, 8, whole_pages=False) == 89
     for bad in ("decode_uniform_0x5", "decode_uniform_3", "decode_512"):
         with pytest.raises(ValueError):
             workloads.by_name(bad)
