@@ -60,9 +60,10 @@ def whole_page(kv_fp8: bool, num_kv_heads: int, split: int) -> bool:
 
 
 def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int = FULL_CHIP_CUS) -> tuple[int, int]:
-    """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes) for the kernels of
-    small steps: CUs x 4 SIMDs x 3 per SIMD for the 16-bit kernel, one per KV head; 2 per SIMD for the fp8
-    kernels, one per two KV heads when they pair up (decode_kernel_name), else one per KV head."""
+    """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes): CUs x 4 SIMDs x 3
+    per SIMD for the 16-bit 4-wavefront kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two
+    KV heads when they pair up (decode_kernel_name), else one per KV head.  fp8 pools size their bins as one
+    round of these."""
     if not kv_fp8:
         return num_cus * 4 * 3, num_kv_heads
     if decode_kernel_name(True, num_heads, num_kv_heads) == "decode_pair_kernel":
@@ -70,22 +71,31 @@ def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int =
     return num_cus * 4 * 2, num_kv_heads
 
 
+SMALL_BIN_PAGES = 16  # the 4-wavefront launch adds workgroups per CU before its bins grow past this
+MIN_SPLIT_PAGES = 2  # the smallest bin the heuristic picks (16-bit pools)
+
+
 def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None = None, kv_fp8: bool = False,
                     num_cus: int = FULL_CHIP_CUS, whole_pages: bool = True) -> int:
-    """Pages per decode bin, so that the step's bins make one round of the decode launch's resident
-    workgroups on a device of `num_cus` CUs.
+    """Pages per decode bin for a step of `decode_pages` decode pages on a device of `num_cus` CUs.
 
     16-bit pools with KV heads in groups of 8 (`whole_pages`): one whole-page workgroup per CU, Hkv / 8 per
     bin, so bins of ceil(T / (rounds x bins per round)) pages, at most 192 (two rounds past 192 x 256 pages).
     That is 134 pages on the 256-row decode workload: 255 bins, 341.7 us against 349.6 us for 383 bins of 89
-    pages in 4-wavefront workgroups (with 257 bins of 133 pages, one bin past a round, 554 us).  When that
-    size is below WHOLE_PAGE_MIN_SPLIT the library runs 4-wavefront workgroups at 3 per SIMD instead, and
-    the bins make one round of those (CUs x 12 wavefronts, one per KV head), at least 8 pages: more rounds of
-    smaller bins measured slower (60 and 45 pages on bf16 decode_256: +10% and +7%), and below 8 pages small
-    steps gain nothing (decode + merge over 8 / 32 / 64 rows of U[128, 4096] tokens took 27 / 56 / 99 us at
-    this size against 30 / 74 / 140 us at 4 pages; 4 rows take ~16.5 us at 1 to 8 pages, launch latency).
-    fp8 pools size their bins for their own kernels' occupancy (67 pages on decode_256 for the pair kernel).
-    `whole_pages=False` gives the 4-wavefront sizing whatever the step."""
+    pages in 4-wavefront workgroups (with 257 bins of 133 pages, one bin past a round, 554 us).
+
+    Below WHOLE_PAGE_MIN_SPLIT the library runs 4-wavefront workgroups (4 KV heads each, up to 3 per CU).
+    Their bins are sized so that no CU gets more than k workgroups: with B = CUs / ceil(Hkv / 4) bins per
+    workgroup round, bins of ceil(T / (k B)) pages, k the fewest (at most 3, all resident) that keeps them
+    within SMALL_BIN_PAGES, and at least MIN_SPLIT_PAGES.  A CU given one workgroup more than the others
+    finishes a bin's time later, and more workgroups per CU than needed only add bins.  Measured on MI355X (append +
+    decode + merge per layer, Llama-3.1-8B heads): 8 to 32 rows of 16-64 pages (T = 128-512) 11.6-14.7 us
+    against 14.6-17.7 us with the previous floor of 8 pages; 256 rows of 16 pages and 64 of 64 (T = 4,096)
+    46.5-48.8 us at 16 pages against 55.2-59.1 us at 11; 32 rows of U[128, 4096] tokens (T = 3,895) 50.8 us
+    against 53.5 us.  Bins that give some CUs one workgroup more measured slower: T = 1,024 at 6 pages
+    (342 workgroups) 24.0 us against 18.3 us at 8 (256).
+    fp8 pools size their bins for their own kernels' occupancy (67 pages on decode_256 for the pair kernel),
+    at least 8 pages.  `whole_pages=False` gives the 4-wavefront sizing whatever the step."""
     forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
     if forced:
         return max(1, min(MAX_SPLIT_PAGES, int(forced)))
@@ -95,8 +105,24 @@ def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None 
         split = math.ceil(decode_pages / (rounds * per_round))
         if split >= WHOLE_PAGE_MIN_SPLIT:
             return split
+    if not kv_fp8:
+        per_round = max(1, num_cus // -(-num_kv_heads // 4))
+        per_cu = min(3, max(1, math.ceil(decode_pages / (per_round * SMALL_BIN_PAGES))))
+        return max(MIN_SPLIT_PAGES, min(MAX_SPLIT_PAGES, math.ceil(decode_pages / (per_round * per_cu))))
     slots, per_bin = decode_waves(num_heads or 4 * num_kv_heads, num_kv_heads, kv_fp8, num_cus)
     return max(8, min(MAX_SPLIT_PAGES, math.ceil(decode_pages * per_bin / slots)))
+
+
+def decode_records_bound(max_pages: int, rows: int, num_kv_heads: int, num_heads: int | None = None,
+                         kv_fp8: bool = False, num_cus: int = FULL_CHIP_CUS, pad_pages: int = 0) -> int:
+    """The most decode plan records a step of `rows` rows and at most `max_pages` decode pages needs at the
+    bin size pages_per_split picks for its page count (plus `pad_pages` pages of padding rows, which do not
+    change that size)."""
+    best = 0
+    for t in range(1, max_pages + 1):
+        c = pages_per_split(t, num_kv_heads, num_heads, kv_fp8, num_cus)
+        best = max(best, decode_plan_size(t + pad_pages, rows, c)[0])
+    return best
 
 
 class PlanOverflowError(RuntimeError):

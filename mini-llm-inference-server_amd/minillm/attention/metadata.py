@@ -267,7 +267,7 @@ class StaticDecodeMetadata:
     them must cover.  The step's split-KV size is staged too (`meta.split_dev`, at least `meta.split_min`
     pages), so the captured plan splits each replayed step as an eager step of the same rows would."""
 
-    SPLIT_MIN = 8  # the smallest split the host heuristic picks
+    SPLIT_MIN = 2  # the smallest split the host heuristic picks (hip_backend.MIN_SPLIT_PAGES)
 
     def __init__(self, num_rows: int, tables: DeviceBlockTables, block_size: int,
                  decode_records: int | None = None) -> None:

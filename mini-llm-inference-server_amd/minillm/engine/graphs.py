@@ -12,9 +12,9 @@ A step then costs the host one packed upload of (num_cached, num_new, block tabl
 one graph launch and the read of B token ids.
 
 The graph is captured with fixed sizes.  A row may hold up to ceil(max_model_len / block_size) blocks;
-the decode plan's capacity of a B-row bucket covers the fewer pages of B rows at that length and the
-whole pool plus one page per row (without prefix sharing, a step's pages never exceed the pool), in
-bins of the smallest split size.  Each replay stages the split size an eager step of the same rows would
+the decode plan's capacity of a B-row bucket covers every step of up to the fewer pages of B rows at that
+length and the whole pool plus one page per row (without prefix sharing, a step's pages never exceed the
+pool), each at the split size the host heuristic picks for its page count.  Each replay stages the split size an eager step of the same rows would
 use (mllm_plan_dev reads it on the device), so a replayed step runs the same decode work as the eager
 one; a step whose plan at that size exceeds the bucket's capacity (rows sharing prefix pages can) is
 not replayed but run eagerly (`fits`).  Every replay fills the plan buffers with -1 before planning,
@@ -28,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from ..attention.hip_backend import MAX_SPLIT_PAGES, device_cus, pages_per_split
+from ..attention.hip_backend import MAX_SPLIT_PAGES, decode_records_bound, device_cus, pages_per_split
 from ..attention.metadata import DeviceBlockTables, SeqStep, StaticDecodeMetadata, decode_plan_size
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
@@ -59,6 +59,7 @@ class DecodeGraphs:
         self.num_heads = model.config.num_attention_heads
         self.head_dim = model.config.head_dim
         self._captured: dict[int, _Captured] = {}
+        self._capacity: dict[int, int] = {}
         self._pool = None
         self._workspace: torch.Tensor | None = None  # shared by every bucket's graph
         self.replays = 0
@@ -72,10 +73,18 @@ class DecodeGraphs:
         return next(b for b in self.buckets if b >= num_rows)
 
     def capacity(self, bucket: int) -> int:
-        """Decode plan records the bucket's plan holds: its rows at max_model_len, or the whole pool plus one
-        page per row, whichever is fewer pages, in bins of SPLIT_MIN pages."""
-        pages = min(bucket * self.tables.max_blocks, self.cache.num_blocks + bucket)
-        return decode_plan_size(pages, bucket, StaticDecodeMetadata.SPLIT_MIN)[0]
+        """Decode plan records the bucket's plan holds: the most any step of `bucket` rows needs (padding rows
+        included) at the split size the heuristic picks for its pages, over steps of up to its rows at
+        max_model_len or the whole pool plus one page per row, whichever is fewer pages.  The captured decode
+        launch covers that many bins, so a bound tighter than every page count at the smallest split keeps
+        the replays' grids small."""
+        cap = self._capacity.get(bucket)
+        if cap is None:
+            pages = min(bucket * self.tables.max_blocks, self.cache.num_blocks + bucket)
+            cap = self._capacity[bucket] = decode_records_bound(
+                pages, bucket, self.num_kv_heads, self.num_heads, self.cache.quantized, device_cus(self.device),
+                pad_pages=bucket)
+        return cap
 
     def fits(self, seqs: list[SeqStep]) -> bool:
         """Whether the decode step `seqs` can replay a graph: a bucket holds its rows, and its decode plan at

@@ -49,11 +49,11 @@ def test_kernel_rates_are_algorithmic_work_over_time():
             return 51_378_782_208
 
     wl = Work()
-    r = {"step_ms": 0.5, "dec_ms": 0.4, "pf_ms": 0.1, "backend_step_ms": 0.45}
+    r = {"step_ms": 0.5, "dec_ms": 0.4, "pf_ms": 0.1, "forward_ms": 0.52}
     out = bench.kernel_rates(wl, r, 2)
     assert out["decode_gbps"] == pytest.approx(2_137_093_012 / 0.4e-3 / 1e9, rel=1e-3)
     assert out["decode_frac_of_8tbps"] == pytest.approx(out["decode_gbps"] / bench.HBM_PEAK_GBPS, rel=1e-3)
     assert out["prefill_tflops"] == pytest.approx(51_378_782_208 / 0.1e-3 / 1e12, rel=1e-3)
     assert out["prefill_frac_of_bf16_peak"] == pytest.approx(out["prefill_tflops"] / bench.BF16_PEAK_TFLOPS, rel=1e-3)
-    assert out["backend_step_us"] == pytest.approx(450.0)
-    assert out["backend_tokens_per_s_32_layers"] == pytest.approx(4476 / (32 * 0.45e-3), rel=1e-3)
+    assert out["step_us"] == pytest.approx(500.0) and out["forward_us"] == pytest.approx(520.0)
+    assert out["tokens"] == 4476 and out["rows"] == 128

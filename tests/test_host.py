@@ -143,8 +143,15 @@ def test_split_size_heuristic(monkeypatch):
     from minillm.attention import hip_backend
 
     monkeypatch.delenv("MLLM_PAGES_PER_SPLIT", raising=False)
-    assert hip_backend.pages_per_split(10, 8) == 8
+    assert hip_backend.pages_per_split(10, 8) == 2  # at least MIN_SPLIT_PAGES
     assert hip_backend.pages_per_split(10 ** 7, 8) == 192
+    # 4-wavefront workgroups (2 per bin at 8 KV heads): the same number on every CU, one while bins stay within
+    # 16 pages, then two, then three; 128 bins fill the 256 CUs once
+    for pages, want, per_cu in ((58, 2, 1), (512, 4, 1), (837, 7, 1), (1024, 8, 1), (2048, 16, 1), (2049, 9, 2),
+                                (3895, 16, 2), (4096, 16, 2), (4097, 11, 3), (5888, 16, 3)):
+        c = hip_backend.pages_per_split(pages, 8)
+        assert c == want and not hip_backend.whole_page(False, 8, c), pages
+        assert math.ceil(pages / c) <= 128 * per_cu and (c == 2 or math.ceil(pages / (c - 1)) > 128 * per_cu), pages
     # whole-page workgroups, one per CU: at most 256 bins, one round
     c = hip_backend.pages_per_split(34000, 8)
     assert c == 133 and math.ceil(34000 / c) <= 256 and math.ceil(34000 / (c - 1)) > 256
