@@ -62,8 +62,8 @@ def whole_page(kv_fp8: bool, num_kv_heads: int, split: int) -> bool:
 def decode_waves(num_heads: int, num_kv_heads: int, kv_fp8: bool, num_cus: int = FULL_CHIP_CUS) -> tuple[int, int]:
     """(resident wavefronts of the decode kernel on the device, wavefronts one bin takes): CUs x 4 SIMDs x 3
     per SIMD for the 16-bit 4-wavefront kernel, one per KV head; 2 per SIMD for the fp8 kernels, one per two
-    KV heads when they pair up (decode_kernel_name), else one per KV head.  fp8 pools size their bins as one
-    round of these."""
+    KV heads when they pair up (decode_kernel_name), else one per KV head.  The fp8 one-head kernel's bins
+    are one round of these."""
     if not kv_fp8:
         return num_cus * 4 * 3, num_kv_heads
     if decode_kernel_name(True, num_heads, num_kv_heads) == "decode_pair_kernel":
@@ -94,8 +94,13 @@ def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None 
     46.5-48.8 us at 16 pages against 55.2-59.1 us at 11; 32 rows of U[128, 4096] tokens (T = 3,895) 50.8 us
     against 53.5 us.  Bins that give some CUs one workgroup more measured slower: T = 1,024 at 6 pages
     (342 workgroups) 24.0 us against 18.3 us at 8 (256).
-    fp8 pools size their bins for their own kernels' occupancy (67 pages on decode_256 for the pair kernel),
-    at least 8 pages.  `whole_pages=False` gives the 4-wavefront sizing whatever the step."""
+    fp8 pools whose KV heads pair up run the pair kernel, whose workgroups (4 wavefronts of two KV heads)
+    also cover 8 KV heads: their bins are sized like whole pages, one workgroup per CU and round, at least
+    MIN_SPLIT_PAGES at any size.  One per CU measured faster than two (the previous rule): decode_256 177.7
+    against 183.3 us (134 against 67 pages a bin), mixed_128's decode 166.4 against 172.6 us, ragged steps
+    of 3,895-25,773 pages 4-13% faster, steps of 128-1,024 pages 12.2-16.9 against 16.6-18.5 us.  The fp8
+    one-head kernel keeps one round of its resident wavefronts, at least 8 pages.  `whole_pages=False`
+    gives the 4-wavefront sizing whatever the step (16-bit pools)."""
     forced = os.environ.get("MLLM_PAGES_PER_SPLIT")
     if forced:
         return max(1, min(MAX_SPLIT_PAGES, int(forced)))
@@ -105,6 +110,10 @@ def pages_per_split(decode_pages: int, num_kv_heads: int, num_heads: int | None 
         split = math.ceil(decode_pages / (rounds * per_round))
         if split >= WHOLE_PAGE_MIN_SPLIT:
             return split
+    if kv_fp8 and decode_kernel_name(True, num_heads or 4 * num_kv_heads, num_kv_heads) == "decode_pair_kernel":
+        per_round = max(1, num_cus // -(-num_kv_heads // WHOLE_PAGE_WAVES))
+        rounds = max(1, math.ceil(decode_pages / (MAX_SPLIT_PAGES * per_round)))
+        return max(MIN_SPLIT_PAGES, min(MAX_SPLIT_PAGES, math.ceil(decode_pages / (rounds * per_round))))
     if not kv_fp8:
         per_round = max(1, num_cus // -(-num_kv_heads // 4))
         per_cu = min(3, max(1, math.ceil(decode_pages / (per_round * SMALL_BIN_PAGES))))

@@ -169,7 +169,11 @@ def test_split_size_heuristic(monkeypatch):
     # KV heads not in groups of 8 never take the whole-page launch
     assert hip_backend.pages_per_split(34000, 4, 32) == math.ceil(34000 * 4 / 3072)
     assert not hip_backend.whole_page(False, 4, 100) and not hip_backend.whole_page(True, 8, 100)
-    assert hip_backend.pages_per_split(34000, 8, 32, kv_fp8=True) == 67  # fp8 pair kernel: 2,048, one per 2 heads
+    # fp8 pair kernel: workgroups of 8 KV heads sized like whole pages, one per CU and round
+    assert hip_backend.pages_per_split(34000, 8, 32, kv_fp8=True) == math.ceil(34000 / 256) == 133
+    assert hip_backend.pages_per_split(65536, 8, 32, kv_fp8=True) == 128  # two rounds past 192 x 256 pages
+    assert hip_backend.pages_per_split(100, 8, 32, kv_fp8=True) == 2
+    assert hip_backend.pages_per_split(4096, 16, 64, kv_fp8=True) == math.ceil(4096 / 128)  # two per bin
     assert hip_backend.pages_per_split(34000, 7, 28, kv_fp8=True) == 117  # fp8 one-head kernel: 2,048, one per head
     monkeypatch.setenv("MLLM_PAGES_PER_SPLIT", "5")
     assert hip_backend.pages_per_split(34000, 8) == 5
@@ -196,7 +200,7 @@ def test_split_size_follows_the_device_cu_count(monkeypatch):
     assert part == math.ceil(10000 / 64) == 157
     assert hip_backend.pages_per_split(10000, 8, 32, False, 256, whole_pages=False) == math.ceil(10000 * 8 / 3072)
     assert hip_backend.pages_per_split(10000, 8, 32, False, 64, whole_pages=False) == math.ceil(10000 * 8 / 768)
-    assert hip_backend.pages_per_split(10000, 8, 32, True, 64) == math.ceil(10000 * 4 / (64 * 8)) == 79
+    assert hip_backend.pages_per_split(10000, 8, 32, True, 64) == math.ceil(10000 / 64) == 157
     assert hip_backend.pages_per_split(40000, 8, 32, False, 64, whole_pages=False) == 192  # clamped
 
 
