@@ -461,6 +461,11 @@ def kernel_rates(wl, r, kv_elem: int) -> dict:
         tf = wl.prefill_flops() / (r["pf_ms"] * 1e-3) / 1e12
         out.update(prefill_us=round(r["pf_ms"] * 1e3, 2), prefill_flops=wl.prefill_flops(),
                    prefill_tflops=round(tf, 1), prefill_frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
+        if r.get("plan") is not None:  # which prefill kernel ran: items of 256 or 128 (token, head) rows
+            from minillm.attention.hip_backend import prefill_kernel_name
+
+            rows = r["plan"].q_tile * (wl.h // wl.hkv)
+            out.update(prefill_kernel=prefill_kernel_name(kv_elem == 1, rows), prefill_rows_per_item=rows)
     out["forward_us"] = round(r["forward_ms"] * 1e3, 2)  # the public forward: checks + allocation + the call
     return out
 
@@ -535,7 +540,8 @@ def main():
         flops = wl.prefill_flops()
         achieved = flops / (pf_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": prefill_kernel_name(fp8),
+                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "kernel": prefill_kernel_name(fp8, r["plan"].q_tile * (wl.h // wl.hkv)),
                     "algorithmic_flops": flops, "mean_us": round(pf_ms * 1e3, 2)}
 
     line = {

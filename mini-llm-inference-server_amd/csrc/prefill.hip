@@ -565,6 +565,236 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
     }
   }
 }
+
+// ---------------------------------------------------------------- the kernel: 4 wavefronts, two per CU
+// prefill4w_kernel: one workgroup of 4 wavefronts per (q tile of 128 rows, KV head), 32 rows per
+// wavefront as above, one 64-key tile per step.  Its LDS is 80 KB (a K ring of three tiles and a V ring
+// of two), and its wavefronts stay within 256 registers, so two workgroups share a CU: while one runs its
+// prologue (record, block ids, first tiles, first scores) or drains its output stores, the other's
+// matrix and vector work keeps the SIMDs busy.  The two wavefronts on a SIMD come from different
+// workgroups and are not phase-locked; the matrix phase runs at raised priority.
+// Step j: the matrix phase runs PV(j) and S(j+1) as one 32-MFMA sequence, then the vector phase the
+// softmax of tile j+1.  At the start of step j the wavefront issues V(j+1) into the V slot of V(j-1) and
+// K(j+3) into the K slot of K(j), both last read in step j-1; the barrier ending step j waits for every
+// load but K(j+3), so step j+1 finds V(j+1) and K(j+2) in LDS.  Block ids are read with scalar loads
+// one step ahead of their DMAs.  16-bit pools only.
+constexpr int kQTileRows4 = 128;  // query rows per workgroup: 4 waves x 32
+constexpr int kRingK4 = 3, kRingV4 = 2;
+constexpr int kVBase4 = kRingK4 * kTileBytes;
+constexpr int kLdsBytes4 = (kRingK4 + kRingV4) * kTileBytes;  // 80 KB: two workgroups fill 160 KB
+
+// This wavefront's share (rows 16 w .. 16 w + 15, the tile's 16-key group w) of the K or V tile at kv0,
+// four DMA instructions of 4 rows.  off[i]: lane offsets from the group base for a full tile.
+template <bool IS_V>
+__device__ __forceinline__ void dma_tile4(const char* pool, const PrefillArgs& a, int blk, int kv0, int last,
+                                          int kv_end, int w, const unsigned (&off)[4], unsigned head_bytes,
+                                          int lane, char* slot) {
+  const unsigned dst = lds_offset(slot) + 16 * w * kRowBytes;
+  if (kv0 + kBN <= kv_end) {
+    const char* base = group_base(pool, a, blk, kv0 + 16 * w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(base, off[i], dst + 4 * i * kRowBytes);
+  } else {  // a row's last tile: keys past `last` load the row of `last` (same block, P = 0)
+    const char* base = group_base(pool, a, blk, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * w + 4 * i + (lane >> 4);
+      const int c = IS_V ? v_chunk(r, lane) : k_chunk(r, lane);
+      const unsigned slot_bytes = (unsigned)(min(kv0 + r, last) & (a.bs - 1)) * (unsigned)a.row_bytes;
+      dma16(base, slot_bytes + head_bytes + 16u * c, dst + 4 * i * kRowBytes);
+    }
+  }
+}
+
+// Online softmax (exp2 domain) of one score tile (keys kv0 .. kv0 + 63) -> the P^T operand of its PV
+// product; the rules of softmax_two (masking, lazy rescale past 2^8, sums over unrounded p) on one tile.
+template <typename T>
+__device__ __forceinline__ void softmax_one(STile& s, u32x4 (&pf)[2][2], f32x16 (&oacc)[4], float& m_run,
+                                            float& l_run, int kv0, int qp, int wave_qp_lo, int h, float c) {
+  if (kv0 + kBN - 1 > wave_qp_lo) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+        s.s[b][r] = key > qp ? -INFINITY : s.s[b][r];
+      }
+  }
+  float m4[4] = {s.s[0][0], s.s[0][1], s.s[0][2], s.s[0][3]};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (b > 0 || r >= 4) m4[r & 3] = __builtin_fmaxf(m4[r & 3], s.s[b][r]);
+  const float mx = max_xor32(__builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3])));
+  if (__any((mx - m_run) * c > 8.f)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2((m_run - m_new) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+    m_run = m_new;
+  }
+  const float mc = m_run * c;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s.s[b][r] = fast_exp2(__builtin_fmaf(s.s[b][r], c, -mc));
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r0 = 8 * u;
+      pf[b][u] = u32x4{pack2<T>(s.s[b][r0 + 0], s.s[b][r0 + 1]), pack2<T>(s.s[b][r0 + 2], s.s[b][r0 + 3]),
+                       pack2<T>(s.s[b][r0 + 4], s.s[b][r0 + 5]), pack2<T>(s.s[b][r0 + 6], s.s[b][r0 + 7])};
+    }
+  float s4[4] = {s.s[0][0], s.s[0][1], s.s[0][2], s.s[0][3]};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (b > 0 || r >= 4) s4[r & 3] += s.s[b][r];
+  l_run += sum_xor32((s4[0] + s4[1]) + (s4[2] + s4[3]));
+}
+
+typedef const __attribute__((address_space(4))) int32_t ConstI32;
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill4w_kernel(
+    const PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int kvh = blockIdx.x % a.Hkv;
+  const int4 w0 = a.work[2 * (blockIdx.x / a.Hkv)], w1 = a.work[2 * (blockIdx.x / a.Hkv) + 1];
+  const int seq = w0.x, t0 = w0.y, qs = w0.z, nn = w0.w, cached = w1.x;
+  if (seq < 0 || w1.z <= 0) return;
+  const int len = cached + nn;
+  ConstI32* pages = (ConstI32*)(a.kv_indices + w1.y);
+  const int tpw = 32 / a.G;
+  const int kv_end = w1.z;
+  const int last = kv_end - 1;
+  const int ntiles = w1.w;
+
+  const int n = lane & 31, h = lane >> 5;
+  const int tok = t0 + wave * tpw + n / a.G;
+  const bool row_valid = tok < nn;
+  const int qp = row_valid ? cached + tok : len - 1;
+  const int wave_tok_hi = min(t0 + wave * tpw + tpw, nn) - 1;
+  const int wave_qp_hi = wave_tok_hi >= t0 + wave * tpw ? cached + wave_tok_hi : -1;
+  const int wave_qp_lo = cached + t0 + wave * tpw;
+  const float c = a.scale_log2;
+
+  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * 2);
+  const unsigned rb = (unsigned)a.row_bytes;
+  unsigned koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * i + (lane >> 4);  // the tile row modulo 16
+    koff[i] = (unsigned)r * rb + head_bytes + 16u * k_chunk(r, lane);
+    voff[i] = (unsigned)r * rb + head_bytes + 16u * v_chunk(r, lane);
+  }
+  const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
+  const unsigned vread = (unsigned)(kVBase4 + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
+
+  const char* kc = reinterpret_cast<const char*>(a.kc);
+  const char* vc = reinterpret_cast<const char*>(a.vc);
+  auto k_slot = [&](int t) { return lds + (t % kRingK4) * kTileBytes; };
+  auto v_slot = [&](int t) { return lds + kVBase4 + (t & (kRingV4 - 1)) * kTileBytes; };
+  // block id of this wavefront's 16-key group of tile t (clamped into the row: always a valid entry)
+  auto blk = [&](int t) { return __builtin_amdgcn_readfirstlane(pages[min(t * kBN + 16 * wu, last) >> a.bs_shift]); };
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // prologue: K(0..2), V(0), then Q; all landed after the first barrier
+  int i1 = blk(1), i2 = blk(2), i3 = blk(3);  // ids of tiles j + 1 .. j + 3 at step j = 0
+  {
+    const int b0 = blk(0);
+    dma_tile4<false>(kc, a, b0, 0, last, kv_end, wu, koff, head_bytes, lane, k_slot(0));
+    dma_tile4<true>(vc, a, b0, 0, last, kv_end, wu, voff, head_bytes, lane, v_slot(0));
+    if (1 < ntiles) dma_tile4<false>(kc, a, i1, kBN, last, kv_end, wu, koff, head_bytes, lane, k_slot(1));
+    if (2 < ntiles) dma_tile4<false>(kc, a, i2, 2 * kBN, last, kv_end, wu, koff, head_bytes, lane, k_slot(2));
+  }
+  u32x4 qf[8];
+  {
+    const int head = kvh * a.G + (n % a.G);
+    const uint16_t* qrow = a.q + (int64_t)(qs + (row_valid ? tok : 0)) * a.q_st + (int64_t)head * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 v = ld16(qrow + 16 * kk + 8 * h);
+      qf[kk] = row_valid ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]), "v"(qf[4]), "v"(qf[5]), "v"(qf[6]), "v"(qf[7])
+               : "memory");
+  barrier_vm<0>();
+
+  STile st;
+  u32x4 pf[2][2];
+  if (0 <= wave_qp_hi) {
+    st = scores<T>(lds, kread, qf);
+    softmax_one<T>(st, pf, oacc, m_run, l_run, 0, qp, wave_qp_lo, h, c);
+  }
+  barrier_lds();  // K(0) has been read: step 0 loads K(3) into its slot
+
+  for (int j = 0; j < ntiles; ++j) {
+    if (j + 1 < ntiles)
+      dma_tile4<true>(vc, a, i1, (j + 1) * kBN, last, kv_end, wu, voff, head_bytes, lane, v_slot(j + 1));
+    const bool k_ahead = j + 3 < ntiles;
+    if (k_ahead) dma_tile4<false>(kc, a, i3, (j + 3) * kBN, last, kv_end, wu, koff, head_bytes, lane, k_slot(j + 3));
+    const int i4 = blk(j + 4);
+    i1 = i2;
+    i2 = i3;
+    i3 = i4;
+    const bool do_pv = j * kBN <= wave_qp_hi, do_s = j + 1 < ntiles && (j + 1) * kBN <= wave_qp_hi;
+    const unsigned vb = vread + (j & (kRingV4 - 1)) * kTileBytes, kb = kread + ((j + 1) % kRingK4) * kTileBytes;
+    __builtin_amdgcn_s_setprio(1);
+    if (do_pv && do_s) {
+      matrix_phase<T>(lds, vb, kb, pf, oacc, st, qf);
+    } else {
+      if (do_pv) pv_tile<T>(lds, vb, pf, oacc);
+      if (do_s) st = scores<T>(lds, kb, qf);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    if (do_s) softmax_one<T>(st, pf, oacc, m_run, l_run, (j + 1) * kBN, qp, wave_qp_lo, h, c);
+    // every load but K(j+3) has landed, and every wavefront is done with V(j) and K(j+1)
+    if (k_ahead)
+      barrier_vm<4>();
+    else
+      barrier_vm<0>();
+  }
+
+  // output: each wavefront's 32 x 128 block transposed through its 8 KB of the K ring (no DMA is in flight
+  // and every wavefront is past its last read of the rings), then whole 16-byte chunks per row
+  const float inv = 1.f / l_run;
+  char* ost = lds + wave * (32 * kRowBytes);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int r = 4 * g4;
+      const u32x2 pk = u32x2{pack2<T>(oacc[dt][r] * inv, oacc[dt][r + 1] * inv),
+                             pack2<T>(oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv)};
+      *reinterpret_cast<u32x2*>(ost + n * kRowBytes + 16 * ((4 * dt + g4) ^ (n & 15)) + 8 * h) = pk;
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4), chunk = lane & 15;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + row * kRowBytes + 16 * (chunk ^ (row & 15)));
+    const int rtok = t0 + wave * tpw + row / a.G;
+    if (rtok < nn) {
+      uint16_t* o = a.out + (int64_t)(qs + rtok) * a.o_st + (int64_t)(kvh * a.G + row % a.G) * a.o_sh;
+      *reinterpret_cast<u32x4*>(o + 8 * chunk) = v;
+    }
+  }
+}
 }  // namespace
 }  // namespace mllm
 
@@ -590,8 +820,10 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
                fn + ": num_heads must be a multiple of num_kv_heads");
   const int G = num_heads / num_kv_heads;
   MLLM_REQUIRE(32 % G == 0, MLLM_ERR_UNSUPPORTED, fn + ": H / Hkv must divide 32");
-  MLLM_REQUIRE(q_tile_tokens == kQTileRows / G, MLLM_ERR_INVALID,
-               fn + ": q_tile_tokens must be 256 / (H / Hkv)");
+  const bool four_waves = q_tile_tokens == kQTileRows4 / G;
+  MLLM_REQUIRE(q_tile_tokens == kQTileRows / G || (four_waves && !fp8), MLLM_ERR_INVALID,
+               fn + (fp8 ? ": q_tile_tokens must be 256 / (H / Hkv)"
+                         : ": q_tile_tokens must be 256 / (H / Hkv) or 128 / (H / Hkv)"));
   MLLM_REQUIRE(num_prefill_work >= 0, MLLM_ERR_INVALID, fn + ": negative count");
   if (num_prefill_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && prefill_work,
@@ -626,7 +858,12 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   a.o_sh = out_stride_head;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
-  if (dtype == MLLM_DTYPE_BF16) {
+  if (four_waves) {  // 128-row items: 4-wavefront workgroups, two per CU
+    if (dtype == MLLM_DTYPE_BF16)
+      prefill4w_kernel<BF16><<<grid, 256, 0, st>>>(a);
+    else
+      prefill4w_kernel<F16><<<grid, 256, 0, st>>>(a);
+  } else if (dtype == MLLM_DTYPE_BF16) {
     if (fp8)
       prefill128_kernel<BF16, true><<<grid, 512, 0, st>>>(a);
     else

@@ -134,6 +134,33 @@ def decode_records_bound(max_pages: int, rows: int, num_kv_heads: int, num_heads
     return best
 
 
+PREFILL_ROWS = 256  # (token, head) rows of a prefill workgroup of 8 wavefronts (one per CU)
+PREFILL_ROWS_SMALL = 128  # rows of a 4-wavefront workgroup (two per CU: 16-bit pools)
+SMALL_PREFILL_PER_CU = 4  # 8-wavefront workgroups per CU up to which 4-wavefront ones are used instead
+
+
+def prefill_q_tile(num_new: list[int], group: int, num_kv_heads: int, kv_fp8: bool = False,
+                   num_cus: int = FULL_CHIP_CUS) -> int:
+    """New tokens per prefill work item: PREFILL_ROWS / group for 8-wavefront workgroups, or
+    PREFILL_ROWS_SMALL / group for 4-wavefront ones, two of which share a CU so that one's prologue and
+    output drain run under the other's main loop.  16-bit pools take the small items when the large ones
+    would give each CU at most SMALL_PREFILL_PER_CU workgroups.  Measured on MI355X (prefill launch,
+    Llama-3.1-8B heads): mixed_128 (2.2 large workgroups per CU) 70.7 against 79.1-79.9 us; steps of
+    4-32 rows of 512-2048 new tokens at 1-4 per CU 2-15% faster; prefix_64 (9.8 per CU) 2% slower, and
+    rows of 256 new tokens over 1,024 cached at 8 and 16 per CU 11% and 26% slower (twice the K/V
+    re-reads per FLOP).  MLLM_PREFILL_ROWS (256 or 128) forces either size.  Group sizes that do not
+    divide 32 have no prefill kernel (the entry point rejects them)."""
+    if 32 % group:
+        return 1
+    forced = os.environ.get("MLLM_PREFILL_ROWS")
+    if forced:
+        small = int(forced) == PREFILL_ROWS_SMALL
+    else:
+        items = sum(-(-nn // (PREFILL_ROWS // group)) for nn in num_new if nn > 1)
+        small = items * num_kv_heads <= SMALL_PREFILL_PER_CU * num_cus
+    return (PREFILL_ROWS_SMALL if small and not kv_fp8 else PREFILL_ROWS) // group
+
+
 class PlanOverflowError(RuntimeError):
     """A decode plan did not fit the capacities it was given (its header reads {0, records, merges, -1})."""
 
@@ -187,11 +214,11 @@ def decode_kernel_name(kv_fp8: bool, num_heads: int, num_kv_heads: int) -> str:
     return "decode_pair_kernel" if pair else "decode_kernel"
 
 
-def prefill_kernel_name(kv_fp8: bool) -> str:
-    """The prefill kernel mllm_paged_prefill(_fp8) launches: phases of two 64-key tiles for every pool type
-    (fp8 tiles pass through registers to be widened on their way into LDS)."""
-    del kv_fp8
-    return "prefill128_kernel"
+def prefill_kernel_name(kv_fp8: bool, q_tile_rows: int = 256) -> str:
+    """The prefill kernel mllm_paged_prefill(_fp8) launches for items of `q_tile_rows` (token, head) rows:
+    8-wavefront workgroups with phases of two 64-key tiles (fp8 tiles pass through registers to be widened
+    on their way into LDS), or 4-wavefront workgroups, two per CU, for 128-row items (16-bit pools)."""
+    return "prefill4w_kernel" if q_tile_rows == PREFILL_ROWS_SMALL and not kv_fp8 else "prefill128_kernel"
 
 
 def is_fp8(pool: torch.Tensor) -> bool:
@@ -452,7 +479,7 @@ class HipBackend(AttentionBackend):
         split_dev = getattr(meta, "split_dev", None)
         c = meta.split_min if split_dev is not None else pages_per_split(decode_pages, hkv, h, kv_fp8, device_cus(dev))
         g = h // hkv
-        q_tile = 256 // g if 32 % g == 0 else 1  # prefill workgroup: 256 (token, head) rows
+        q_tile = prefill_q_tile(news, g, hkv, kv_fp8, device_cus(dev))
         decode_rows = sum(1 for nn in news if nn == 1)
         n_dec, n_merge = decode_plan_size(decode_pages, decode_rows, c)
         if split_dev is not None:  # a captured step sized for fewer records than its worst case

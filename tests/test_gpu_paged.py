@@ -128,12 +128,36 @@ def test_metadata_workloads(hip, name):
 # ------------------------------------------------------------------ append + attention on the workloads
 
 
-@pytest.mark.parametrize("name", ["decode_4", "decode_256", "mixed_128", "prefix_64"])
+@pytest.fixture(params=[256, 128], ids=["rows256", "rows128"])
+def prefill_rows(request, monkeypatch):
+    """Forces the prefill items to 256 (token, head) rows (8-wavefront workgroups) or 128 (4-wavefront
+    workgroups, two per CU), whatever the host's choice for the step."""
+    monkeypatch.setenv("MLLM_PREFILL_ROWS", str(request.param))
+    return request.param
+
+
+@pytest.mark.parametrize("name", ["decode_4", "decode_256"])
 def test_workload_parity(hip, name):
     from minillm import workloads
 
     wl = workloads.WORKLOADS[name]()
     out, pk, pv, _ = hip_step(wl, DEV)
+    ref, rk, rv = oracle_step(wl, DEV)
+    assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("name", ["mixed_128", "prefix_64"])
+def test_prefill_workload_parity(hip, name, prefill_rows):
+    # both prefill kernels on the two prefill workloads: pools bit-exact, outputs within tolerance
+    from minillm import workloads
+    from minillm.attention.hip_backend import HipBackend
+
+    wl = workloads.WORKLOADS[name]()
+    backend = HipBackend()
+    out, pk, pv, _ = hip_step(wl, DEV, backend=backend)
+    assert backend._plan.q_tile * (wl.h // wl.hkv) == prefill_rows
     ref, rk, rv = oracle_step(wl, DEV)
     assert torch.equal(bits(pk), bits(rk)) and torch.equal(bits(pv), bits(rv))
     assert torch.isfinite(out).all()
@@ -305,7 +329,7 @@ def test_larger_blocks(hip, bs):
 
 
 @pytest.mark.parametrize("h,hkv", [(32, 1), (64, 2)], ids=["g32", "g32-hkv2"])
-def test_prefill_group_32(hip, h, hkv):
+def test_prefill_group_32(hip, prefill_rows, h, hkv):
     # 32 query heads per KV head: decode does not take it, prefill does (one token per wavefront, 8 per
     # q tile); rows with several new tokens only, fresh and cached, lengths not tile-aligned
     steps = [(0, 37), (40, 25), (17, 70), (300, 2), (129, 130), (0, 9)]
@@ -317,7 +341,7 @@ def test_prefill_group_32(hip, h, hkv):
 
 
 @pytest.mark.parametrize("bs", [128, 256])
-def test_blocks_of_several_key_tiles(hip, bs):
+def test_blocks_of_several_key_tiles(hip, prefill_rows, bs):
     # a page of 128 or 256 tokens holds 2 or 4 of the prefill kernel's 64-key tiles and 8 or 16 of
     # decode's 16-token tiles; rows of every kind, prefixes past one page and past several
     steps = [(0, 37), (90, 1), (40, 25), (0, 1), (300, 1), (129, 130), (700, 300), (1000, 1), (255, 2)]
@@ -329,7 +353,7 @@ def test_blocks_of_several_key_tiles(hip, bs):
     torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
-def test_prefill_tile_and_pair_boundaries(hip):
+def test_prefill_tile_and_pair_boundaries(hip, prefill_rows):
     # the prefill kernel runs 64-key tiles in pairs: rows whose visible keys end one before, on and one
     # after a tile, pair and q-tile boundary (odd and even tile counts, a pair's second tile past the row
     # or past a wavefront's last row), with 2 to 65 new tokens
@@ -347,7 +371,7 @@ def test_prefill_tile_and_pair_boundaries(hip):
 
 
 @pytest.mark.parametrize("seed", range(4))
-def test_random_mixed_steps(hip, seed):
+def test_random_mixed_steps(hip, prefill_rows, seed):
     # seeded random steps with every row kind (fresh and cached, one and many new tokens, lengths not
     # page-aligned) at the Llama GQA shape: the prefill items of many lengths exercise the plan's
     # longest-first order and record fields; pools bit-exact, outputs within tolerance of the oracle
@@ -676,6 +700,11 @@ def test_prefill_item_without_visible_keys_writes_nothing(hip):
     lib.call("mllm_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), pool.data_ptr(), nb, bs,
              h, hkv, dh, qo.data_ptr(), kvp.data_ptr(), kvi.data_ptr(), lens.data_ptr(), rec.data_ptr(), 1,
              256 // (h // hkv), dh ** -0.5, _native.dtype_code(torch.bfloat16), out.data_ptr(), out.stride(0),
+             out.stride(1), _native.stream_ptr(torch.device(DEV)))
+    # the same record as a 128-row item (4-wavefront workgroups)
+    lib.call("mllm_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), pool.data_ptr(), nb, bs,
+             h, hkv, dh, qo.data_ptr(), kvp.data_ptr(), kvi.data_ptr(), lens.data_ptr(), rec.data_ptr(), 1,
+             128 // (h // hkv), dh ** -0.5, _native.dtype_code(torch.bfloat16), out.data_ptr(), out.stride(0),
              out.stride(1), _native.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
