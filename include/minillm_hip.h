@@ -231,9 +231,9 @@ int mllm_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_str
  * chunk, bottom-right aligned over the cached prefix, K/V read through kv_indices.  QK^T and PV on
  * bf16/fp16 MFMA (32x32x16) with fp32 online softmax; the H/Hkv query heads of one KV head share
  * each K/V tile.  Work items from mllm_plan (prefill_work) with q_tile_tokens = 256 / (H / Hkv): one
- * workgroup of 8 wavefronts per (item, KV head), one per CU; or, 16-bit pools only, q_tile_tokens =
- * 128 / (H / Hkv): workgroups of 4 wavefronts, two per CU (for steps of few items: one workgroup's
- * prologue and output drain run under the other's main loop).  Other q_tile_tokens values are rejected.
+ * workgroup of 8 wavefronts per (item, KV head), one per CU; or q_tile_tokens = 128 / (H / Hkv):
+ * workgroups of 4 wavefronts, two per CU (for steps of few items: one workgroup's prologue and output
+ * drain run under the other's main loop).  Other q_tile_tokens values are rejected.
  * Same shape limits as mllm_paged_decode, and H / Hkv must divide 32; q, out and their row strides
  * 16-byte aligned.
  */
@@ -342,7 +342,7 @@ int mllm_paged_decode_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_
                           void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
-/* mllm_paged_prefill over an fp8 pool (q_tile_tokens = 256 / (H / Hkv) only). */
+/* mllm_paged_prefill over an fp8 pool. */
 int mllm_paged_prefill_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                            const void* v_cache, int64_t num_blocks, int32_t block_size, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, const int32_t* qo_indptr, const int32_t* kv_indptr,

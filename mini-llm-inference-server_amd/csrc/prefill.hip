@@ -577,7 +577,10 @@ __global__ __launch_bounds__(512) void prefill128_kernel(const PrefillArgs a) {
 // softmax of tile j+1.  At the start of step j the wavefront issues V(j+1) into the V slot of V(j-1) and
 // K(j+3) into the K slot of K(j), both last read in step j-1; the barrier ending step j waits for every
 // load but K(j+3), so step j+1 finds V(j+1) and K(j+2) in LDS.  Block ids are read with scalar loads
-// one step ahead of their DMAs.  16-bit pools only.
+// one step ahead of their loads.
+// fp8 pools: the same two tiles are loaded into VGPRs at the start of step j (two 16-byte loads per lane
+// each: the wavefront's 16 rows of 128 bytes) and widened into their LDS slots at its end, before the
+// barrier; the slots were last read in step j-1.
 constexpr int kQTileRows4 = 128;  // query rows per workgroup: 4 waves x 32
 constexpr int kRingK4 = 3, kRingV4 = 2;
 constexpr int kVBase4 = kRingK4 * kTileBytes;
@@ -659,7 +662,7 @@ __device__ __forceinline__ void softmax_one(STile& s, u32x4 (&pf)[2][2], f32x16 
 
 typedef const __attribute__((address_space(4))) int32_t ConstI32;
 
-template <typename T>
+template <typename T, bool F8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill4w_kernel(
     const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes4];
@@ -687,7 +690,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wave_qp_lo = cached + t0 + wave * tpw;
   const float c = a.scale_log2;
 
-  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * 2);
+  const unsigned head_bytes = (unsigned)(kvh * kHeadDim * (F8 ? 1 : 2));
   const unsigned rb = (unsigned)a.row_bytes;
   unsigned koff[4], voff[4];
 #pragma unroll
@@ -696,6 +699,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     koff[i] = (unsigned)r * rb + head_bytes + 16u * k_chunk(r, lane);
     voff[i] = (unsigned)r * rb + head_bytes + 16u * v_chunk(r, lane);
   }
+  // fp8: this wavefront's rows as two 8-row shares (those of wavefront 2 w + i of the 8-wavefront layout)
+  const unsigned soff0 = (unsigned)(lane >> 3) * rb + head_bytes + 16u * (lane & 7), soff1 = soff0 + 8 * rb;
+  auto stage2 = [&](const char* pool, int b, int t, u32x4 (&x)[2]) {
+    x[0] = stage_load(pool, a, b, t * kBN, last, kv_end, 2 * wu, soff0, head_bytes, lane);
+    x[1] = stage_load(pool, a, b, t * kBN, last, kv_end, 2 * wu + 1, soff1, head_bytes, lane);
+  };
+  auto store2 = [&](bool is_v, const u32x4 (&x)[2], char* slot) {
+    if (is_v) {
+      stage_store<T, true>(x[0], 2 * wu, lane, slot);
+      stage_store<T, true>(x[1], 2 * wu + 1, lane, slot);
+    } else {
+      stage_store<T, false>(x[0], 2 * wu, lane, slot);
+      stage_store<T, false>(x[1], 2 * wu + 1, lane, slot);
+    }
+  };
   const unsigned kread = (unsigned)(n * kRowBytes + 16 * (h ^ (n & 1)) + 32 * ((n & 15) >> 1));
   const unsigned vread = (unsigned)(kVBase4 + 1024 * h + 320 * ((lane >> 2) & 3) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
 
@@ -715,7 +733,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // prologue: K(0..2), V(0), then Q; all landed after the first barrier
   int i1 = blk(1), i2 = blk(2), i3 = blk(3);  // ids of tiles j + 1 .. j + 3 at step j = 0
-  {
+  if constexpr (F8) {
+    const int b0 = blk(0);
+    u32x4 k0[2], v0[2], k1[2], k2[2];
+    stage2(kc, b0, 0, k0);
+    stage2(vc, b0, 0, v0);
+    if (1 < ntiles) stage2(kc, i1, 1, k1);
+    if (2 < ntiles) stage2(kc, i2, 2, k2);
+    store2(false, k0, k_slot(0));
+    store2(true, v0, v_slot(0));
+    if (1 < ntiles) store2(false, k1, k_slot(1));
+    if (2 < ntiles) store2(false, k2, k_slot(2));
+  } else {
     const int b0 = blk(0);
     dma_tile4<false>(kc, a, b0, 0, last, kv_end, wu, koff, head_bytes, lane, k_slot(0));
     dma_tile4<true>(vc, a, b0, 0, last, kv_end, wu, voff, head_bytes, lane, v_slot(0));
@@ -744,11 +773,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   barrier_lds();  // K(0) has been read: step 0 loads K(3) into its slot
 
+  u32x4 sv[2] = {}, sk[2] = {};  // fp8: V(j+1) and K(j+3) on their way through registers
   for (int j = 0; j < ntiles; ++j) {
-    if (j + 1 < ntiles)
-      dma_tile4<true>(vc, a, i1, (j + 1) * kBN, last, kv_end, wu, voff, head_bytes, lane, v_slot(j + 1));
-    const bool k_ahead = j + 3 < ntiles;
-    if (k_ahead) dma_tile4<false>(kc, a, i3, (j + 3) * kBN, last, kv_end, wu, koff, head_bytes, lane, k_slot(j + 3));
+    const bool v_ahead = j + 1 < ntiles, k_ahead = j + 3 < ntiles;
+    if constexpr (F8) {
+      if (v_ahead) stage2(vc, i1, j + 1, sv);
+      if (k_ahead) stage2(kc, i3, j + 3, sk);
+    } else {
+      if (v_ahead)
+        dma_tile4<true>(vc, a, i1, (j + 1) * kBN, last, kv_end, wu, voff, head_bytes, lane, v_slot(j + 1));
+      if (k_ahead)
+        dma_tile4<false>(kc, a, i3, (j + 3) * kBN, last, kv_end, wu, koff, head_bytes, lane, k_slot(j + 3));
+    }
     const int i4 = blk(j + 4);
     i1 = i2;
     i2 = i3;
@@ -764,16 +800,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __builtin_amdgcn_s_setprio(0);
     if (do_s) softmax_one<T>(st, pf, oacc, m_run, l_run, (j + 1) * kBN, qp, wave_qp_lo, h, c);
-    // every load but K(j+3) has landed, and every wavefront is done with V(j) and K(j+1)
-    if (k_ahead)
+    if constexpr (F8) {  // widened into the slots of V(j-1) and K(j), both last read in step j-1
+      if (v_ahead) store2(true, sv, v_slot(j + 1));
+      if (k_ahead) store2(false, sk, k_slot(j + 3));
+      barrier_lds();
+    } else if (k_ahead) {  // every load but K(j+3) has landed, and every wavefront is done with V(j), K(j+1)
       barrier_vm<4>();
-    else
+    } else {
       barrier_vm<0>();
+    }
   }
 
   // output: each wavefront's 32 x 128 block transposed through its 8 KB of the K ring (no DMA is in flight
   // and every wavefront is past its last read of the rings), then whole 16-byte chunks per row
-  const float inv = 1.f / l_run;
+  const float inv = (F8 ? a.v_scale : 1.f) / l_run;
   char* ost = lds + wave * (32 * kRowBytes);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -821,9 +861,8 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   const int G = num_heads / num_kv_heads;
   MLLM_REQUIRE(32 % G == 0, MLLM_ERR_UNSUPPORTED, fn + ": H / Hkv must divide 32");
   const bool four_waves = q_tile_tokens == kQTileRows4 / G;
-  MLLM_REQUIRE(q_tile_tokens == kQTileRows / G || (four_waves && !fp8), MLLM_ERR_INVALID,
-               fn + (fp8 ? ": q_tile_tokens must be 256 / (H / Hkv)"
-                         : ": q_tile_tokens must be 256 / (H / Hkv) or 128 / (H / Hkv)"));
+  MLLM_REQUIRE(q_tile_tokens == kQTileRows / G || four_waves, MLLM_ERR_INVALID,
+               fn + ": q_tile_tokens must be 256 / (H / Hkv) or 128 / (H / Hkv)");
   MLLM_REQUIRE(num_prefill_work >= 0, MLLM_ERR_INVALID, fn + ": negative count");
   if (num_prefill_work == 0) return MLLM_OK;
   MLLM_REQUIRE(q && k_cache && v_cache && out && qo_indptr && kv_indptr && kv_indices && seq_lens && prefill_work,
@@ -859,10 +898,17 @@ int paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, co
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)num_prefill_work * (unsigned)num_kv_heads;
   if (four_waves) {  // 128-row items: 4-wavefront workgroups, two per CU
-    if (dtype == MLLM_DTYPE_BF16)
-      prefill4w_kernel<BF16><<<grid, 256, 0, st>>>(a);
-    else
-      prefill4w_kernel<F16><<<grid, 256, 0, st>>>(a);
+    if (dtype == MLLM_DTYPE_BF16) {
+      if (fp8)
+        prefill4w_kernel<BF16, true><<<grid, 256, 0, st>>>(a);
+      else
+        prefill4w_kernel<BF16, false><<<grid, 256, 0, st>>>(a);
+    } else {
+      if (fp8)
+        prefill4w_kernel<F16, true><<<grid, 256, 0, st>>>(a);
+      else
+        prefill4w_kernel<F16, false><<<grid, 256, 0, st>>>(a);
+    }
   } else if (dtype == MLLM_DTYPE_BF16) {
     if (fp8)
       prefill128_kernel<BF16, true><<<grid, 512, 0, st>>>(a);

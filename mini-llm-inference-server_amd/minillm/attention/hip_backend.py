@@ -143,13 +143,14 @@ def prefill_q_tile(num_new: list[int], group: int, num_kv_heads: int, kv_fp8: bo
                    num_cus: int = FULL_CHIP_CUS) -> int:
     """New tokens per prefill work item: PREFILL_ROWS / group for 8-wavefront workgroups, or
     PREFILL_ROWS_SMALL / group for 4-wavefront ones, two of which share a CU so that one's prologue and
-    output drain run under the other's main loop.  16-bit pools take the small items when the large ones
-    would give each CU at most SMALL_PREFILL_PER_CU workgroups.  Measured on MI355X (prefill launch,
-    Llama-3.1-8B heads): mixed_128 (2.2 large workgroups per CU) 70.7 against 79.1-79.9 us; steps of
-    4-32 rows of 512-2048 new tokens at 1-4 per CU 2-15% faster; prefix_64 (9.8 per CU) 2% slower, and
-    rows of 256 new tokens over 1,024 cached at 8 and 16 per CU 11% and 26% slower (twice the K/V
-    re-reads per FLOP).  MLLM_PREFILL_ROWS (256 or 128) forces either size.  Group sizes that do not
-    divide 32 have no prefill kernel (the entry point rejects them)."""
+    output drain run under the other's main loop.  A step takes the small items when the large ones would
+    give each CU at most SMALL_PREFILL_PER_CU workgroups.  Measured on MI355X (prefill launch,
+    Llama-3.1-8B heads): mixed_128 (2.2 large workgroups per CU) 70.7 against 79.1-79.9 us, on an fp8
+    pool 79.2 against 84.5-86.4 us; steps of 4-32 rows of 512-2048 new tokens at 1-4 per CU 2-15%
+    faster; prefix_64 (9.8 per CU) 2% slower on either pool, and rows of 256 new tokens over 1,024
+    cached at 8 and 16 per CU 11% and 26% slower (twice the K/V re-reads per FLOP).  MLLM_PREFILL_ROWS
+    (256 or 128) forces either size.  Group sizes that do not divide 32 have no prefill kernel (the entry
+    point rejects them)."""
     if 32 % group:
         return 1
     forced = os.environ.get("MLLM_PREFILL_ROWS")
@@ -158,7 +159,7 @@ def prefill_q_tile(num_new: list[int], group: int, num_kv_heads: int, kv_fp8: bo
     else:
         items = sum(-(-nn // (PREFILL_ROWS // group)) for nn in num_new if nn > 1)
         small = items * num_kv_heads <= SMALL_PREFILL_PER_CU * num_cus
-    return (PREFILL_ROWS_SMALL if small and not kv_fp8 else PREFILL_ROWS) // group
+    return (PREFILL_ROWS_SMALL if small else PREFILL_ROWS) // group
 
 
 class PlanOverflowError(RuntimeError):
@@ -216,9 +217,10 @@ def decode_kernel_name(kv_fp8: bool, num_heads: int, num_kv_heads: int) -> str:
 
 def prefill_kernel_name(kv_fp8: bool, q_tile_rows: int = 256) -> str:
     """The prefill kernel mllm_paged_prefill(_fp8) launches for items of `q_tile_rows` (token, head) rows:
-    8-wavefront workgroups with phases of two 64-key tiles (fp8 tiles pass through registers to be widened
-    on their way into LDS), or 4-wavefront workgroups, two per CU, for 128-row items (16-bit pools)."""
-    return "prefill4w_kernel" if q_tile_rows == PREFILL_ROWS_SMALL and not kv_fp8 else "prefill128_kernel"
+    8-wavefront workgroups with phases of two 64-key tiles, or 4-wavefront workgroups, two per CU, for
+    128-row items (on fp8 pools both pass tiles through registers to be widened on their way into LDS)."""
+    del kv_fp8
+    return "prefill4w_kernel" if q_tile_rows == PREFILL_ROWS_SMALL else "prefill128_kernel"
 
 
 def is_fp8(pool: torch.Tensor) -> bool:

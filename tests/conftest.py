@@ -32,3 +32,11 @@ def hip():
 
     HipBackend.check_plan = True  # every plan a GPU test builds through the backend must fit its capacities
     return _native.lib()
+
+
+@pytest.fixture(params=[256, 128], ids=["rows256", "rows128"])
+def prefill_rows(request, monkeypatch):
+    """Forces the prefill items to 256 (token, head) rows (8-wavefront workgroups) or 128 (4-wavefront
+    workgroups, two per CU), whatever the host's choice for the step."""
+    monkeypatch.setenv("MLLM_PREFILL_ROWS", str(request.param))
+    return request.param

@@ -128,14 +128,6 @@ def test_metadata_workloads(hip, name):
 # ------------------------------------------------------------------ append + attention on the workloads
 
 
-@pytest.fixture(params=[256, 128], ids=["rows256", "rows128"])
-def prefill_rows(request, monkeypatch):
-    """Forces the prefill items to 256 (token, head) rows (8-wavefront workgroups) or 128 (4-wavefront
-    workgroups, two per CU), whatever the host's choice for the step."""
-    monkeypatch.setenv("MLLM_PREFILL_ROWS", str(request.param))
-    return request.param
-
-
 @pytest.mark.parametrize("name", ["decode_4", "decode_256"])
 def test_workload_parity(hip, name):
     from minillm import workloads

@@ -117,7 +117,7 @@ def test_attention_forward_argument_errors(libpath):
 
 def test_prefill_item_size(monkeypatch, libpath):
     # 128-row items (4-wavefront workgroups, two per CU) when 256-row ones would give each CU at most 4
-    # workgroups; 16-bit pools only; MLLM_PREFILL_ROWS forces either; the entry points check the size
+    # workgroups, on either pool; MLLM_PREFILL_ROWS forces either; the entry points check the size
     from minillm import _native
     from minillm.attention import hip_backend as hb
 
@@ -127,13 +127,13 @@ def test_prefill_item_size(monkeypatch, libpath):
     assert hb.prefill_q_tile([64] * 129, 4, 8) == 64
     assert hb.prefill_q_tile([2048] * 16, 4, 8) == 64
     assert hb.prefill_q_tile([64] * 32, 4, 8, num_cus=64) == 32 and hb.prefill_q_tile([64] * 33, 4, 8, num_cus=64) == 64
-    assert hb.prefill_q_tile([512] * 8, 4, 8, kv_fp8=True) == 64
+    assert hb.prefill_q_tile([512] * 8, 4, 8, kv_fp8=True) == 32 and hb.prefill_q_tile([2048] * 16, 4, 8, True) == 64
     assert hb.prefill_q_tile([512] * 8, 8, 8) == 16 and hb.prefill_q_tile([512] * 8, 3, 8) == 1
-    assert hb.prefill_kernel_name(False, 128) == "prefill4w_kernel" and hb.prefill_kernel_name(True, 128) == "prefill128_kernel"
+    assert hb.prefill_kernel_name(True, 128) == "prefill4w_kernel" and hb.prefill_kernel_name(False, 256) == "prefill128_kernel"
     monkeypatch.setenv("MLLM_PREFILL_ROWS", "256")
     assert hb.prefill_q_tile([512] * 8, 4, 8) == 64
     monkeypatch.setenv("MLLM_PREFILL_ROWS", "128")
-    assert hb.prefill_q_tile([2048] * 16, 4, 8) == 32 and hb.prefill_q_tile([2048] * 16, 4, 8, kv_fp8=True) == 64
+    assert hb.prefill_q_tile([2048] * 16, 4, 8) == 32 and hb.prefill_q_tile([2048] * 16, 4, 8, kv_fp8=True) == 32
     lib = _native.lib()
     shape = (0, 0, 0, 0, 0, 64, 16, 32, 8, 128, 0, 0, 0, 0, 0, 0)  # q .. prefill_work, no items
 
@@ -144,8 +144,9 @@ def test_prefill_item_size(monkeypatch, libpath):
     call("mllm_paged_prefill", 32)  # no items: returns before any launch
     with pytest.raises(ValueError, match="256 / \\(H / Hkv\\) or 128"):
         call("mllm_paged_prefill", 48)
-    with pytest.raises(ValueError, match="q_tile_tokens must be 256 / \\(H / Hkv\\)$"):
-        call("mllm_paged_prefill_fp8", 32, 1.0, 1.0)
+    call("mllm_paged_prefill_fp8", 32, 1.0, 1.0)
+    with pytest.raises(ValueError, match="256 / \\(H / Hkv\\) or 128"):
+        call("mllm_paged_prefill_fp8", 16, 1.0, 1.0)
 
 
 def ctypes_addr(obj) -> int:
